@@ -1,0 +1,90 @@
+/*
+ * C ABI of the MI355X (gfx950) INT4 weight-only linear library, libkf_int4.so.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*; NULL is the legacy default stream).  Nothing here
+ * allocates device memory, synchronizes, or reads device memory from the
+ * host, so every call is asynchronous and safe under hipGraph stream capture.
+ * Outputs and the split-K workspace are owned by the caller.
+ *
+ * Data layout (the reference's packing convention, kernelforge/quantize.py:12-24):
+ *   x       fp16  [M, K]    row-major, contiguous
+ *   packed  int32 [N, K/8]  row-major; word j of row n holds u = q + 8 for
+ *                           k = 8j..8j+7 with nibble p (bits 4p..4p+3) = k offset
+ *                           (0,2,4,6,1,3,5,7)[p]
+ *   scales  fp16  [N, K/G]  row-major
+ *   y       fp16  [M, N]    row-major
+ * y[m, n] = fp16_rne( sum_k x[m, k] * W_hat[n, k] ) with fp32 accumulation,
+ * W_hat = fp16_rne(q * s) (GEMM path) or q * s folded per 32-k chunk (GEMV).
+ *
+ * Return value: KF_OK (0) or one of the KF_ERR_* codes; kf_last_error()
+ * returns a thread-local message describing the most recent failure.
+ */
+#ifndef KF_INT4_H_
+#define KF_INT4_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_ABI_VERSION 1
+
+enum kf_status {
+  KF_OK = 0,
+  KF_ERR_INVALID_ARG = 1,   /* null pointer, misaligned pointer, bad M/N/K/G */
+  KF_ERR_UNSUPPORTED = 2,   /* valid arguments outside this kernel's domain */
+  KF_ERR_WORKSPACE = 3,     /* split-K workspace missing or too small */
+  KF_ERR_HIP = 4,           /* HIP runtime error (launch failure, bad device) */
+};
+
+/* Version of this ABI (KF_ABI_VERSION). No reference counterpart. */
+int kf_abi_version(void);
+
+/* Message for the most recent non-zero status on the calling thread.
+ * Replaces the reference's exception text (csrc/common/check.cuh:8-24,
+ * TORCH_CHECK in csrc/gemm/dequant_gemv.cu:5-19). */
+const char* kf_last_error(void);
+
+/* Fused dequant GEMV for M in [1, 8], any N >= 1, K % G == 0, G in {64, 128}.
+ * x and packed must be 16-byte aligned.
+ * Replaces kf::gemv::dispatch (csrc/gemm/dequant_gemv_kernel.cuh:120-142)
+ * and the pybind entry _C.int4_gemv (csrc/bindings.cpp:24-25,
+ * csrc/gemm/dequant_gemv.cu:21-36). */
+int kf_int4_gemv(const void* x, const void* packed, const void* scales, void* y,
+                 int M, int N, int K, int group_size, void* stream);
+
+/* Bytes of fp32 split-K workspace kf_int4_gemm needs for this problem on the
+ * current device (0 when the chosen plan has no split-K).
+ * Replaces kf::gemm_tc::workspace_floats (dequant_gemm_tc_kernel.cuh:179-183),
+ * which counted floats instead of bytes. */
+size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size);
+
+/* MFMA dequant GEMM, any M >= 1, N % 64 == 0, K % G == 0, G in {64, 128}.
+ * ws may be NULL when kf_int4_gemm_workspace_bytes() returned 0.
+ * Replaces kf::gemm_tc::run (dequant_gemm_tc_kernel.cuh:203-211) and the
+ * pybind entry _C.int4_gemm (csrc/bindings.cpp:26-27,
+ * csrc/gemm/dequant_gemm_tc.cu:7-28). */
+int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
+                 void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream);
+
+/* W_hat = fp16_rne(q * s) as fp16 [N, K]: the dequantization the GEMM feeds
+ * to the matrix cores, exported so it can be compared bit for bit with the
+ * reference's dequantize(qw, torch.float16) (kernelforge/quantize.py:108-113). */
+int kf_int4_dequant_fp16(const void* packed, const void* scales, void* w_hat,
+                         int N, int K, int group_size, void* stream);
+
+/* Streaming HBM ceilings with dwordx4 accesses: dst[i] = src[i] (copy),
+ * a checksum of src folded into sink[0..grid) (read), dst[i] = pattern
+ * (write).  bytes must be a multiple of 16.  grid_blocks <= 0 picks a default.
+ * Replace the reference's measurement kernels (csrc/micro/bandwidth.cu:17-42). */
+int kf_bw_copy(const void* src, void* dst, size_t bytes, int grid_blocks, void* stream);
+int kf_bw_read(const void* src, void* sink, size_t bytes, int grid_blocks, void* stream);
+int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KF_INT4_H_ */

@@ -1,0 +1,170 @@
+// extern "C" entry points of libkf_int4.so (declared in include/kf_int4.h).
+//
+// This layer validates arguments (the checks of the reference's
+// int4_check_inputs, csrc/gemm/dequant_gemv.cu:5-19, and of
+// csrc/gemm/dequant_gemm_tc.cu:9-14), maps failures to status codes plus a
+// thread-local message, and launches on the caller's stream.  It never
+// allocates, synchronizes, or reads device memory, so it is safe inside
+// hipGraph stream capture.
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "kf_int4.h"
+#include "kf_launch.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return KF_OK;
+  return fail(KF_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(err), hipGetErrorString(err));
+}
+
+// Compute-unit count of the current device, queried once per device.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count(int* out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(KF_ERR_HIP, "device ordinal %d out of range", dev);
+  int cus = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return hip_status(err, "hipDeviceGetAttribute(MultiprocessorCount)");
+    g_cu_count[dev].store(cus, std::memory_order_relaxed);
+  }
+  *out = cus;
+  return KF_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Checks shared by the GEMV and the GEMM (order and wording follow
+// kernelforge/ops.py:171-182 and csrc/gemm/dequant_gemv.cu:5-19).
+int check_common(const void* x, const void* packed, const void* scales, const void* y, int M, int N, int K,
+                 int group_size) {
+  if (!x || !packed || !scales || !y) return fail(KF_ERR_INVALID_ARG, "x, packed, scales and y must be non-null");
+  if (M < 1 || N < 1 || K < 1) return fail(KF_ERR_INVALID_ARG, "M, N, K must be positive, got M=%d N=%d K=%d", M, N, K);
+  if (group_size != 64 && group_size != 128)
+    return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);
+  if (K % group_size != 0)
+    return fail(KF_ERR_INVALID_ARG, "K=%d is not a multiple of group_size=%d", K, group_size);
+  if (!aligned(x, 16) || !aligned(packed, 16))
+    return fail(KF_ERR_INVALID_ARG, "x and packed must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(y, 2)) return fail(KF_ERR_INVALID_ARG, "scales and y must be 2-byte aligned");
+  return KF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kf_abi_version(void) { return KF_ABI_VERSION; }
+
+const char* kf_last_error(void) { return g_error; }
+
+int kf_int4_gemv(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
+                 int group_size, void* stream) {
+  int st = check_common(x, packed, scales, y, M, N, K, group_size);
+  if (st) return st;
+  if (M > 8) return fail(KF_ERR_INVALID_ARG, "int4_gemv handles M in [1, 8], got M=%d", M);
+  int cus = 0;
+  if ((st = cu_count(&cus))) return st;
+  const kf::GemvPlan plan = kf::gemv_plan(M, N, K, cus);
+  return hip_status(kf::gemv_launch(plan, x, packed, scales, y, M, N, K, group_size,
+                                    static_cast<hipStream_t>(stream)),
+                    "int4_gemv launch");
+}
+
+size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size) {
+  if (M < 1 || N < 1 || K < 64 || K % 64 || (group_size != 64 && group_size != 128)) return 0;
+  int cus = 0;
+  if (cu_count(&cus)) return 0;
+  return kf::gemm_workspace_bytes(kf::gemm_plan(M, N, K, cus), M, N);
+}
+
+int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y, void* ws, size_t ws_bytes, int M,
+                 int N, int K, int group_size, void* stream) {
+  int st = check_common(x, packed, scales, y, M, N, K, group_size);
+  if (st) return st;
+  if (N % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs N to be a multiple of 64, got N=%d", N);
+  if (K % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs K to be a multiple of 64, got K=%d", K);
+  int cus = 0;
+  if ((st = cu_count(&cus))) return st;
+  const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);
+  if ((long)(M + plan.block_m - 1) / plan.block_m > 65535)
+    return fail(KF_ERR_UNSUPPORTED, "M=%d exceeds the grid limit for a %d-row tile", M, plan.block_m);
+  const size_t need = kf::gemm_workspace_bytes(plan, M, N);
+  if (need > 0) {
+    if (!ws) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got NULL", need);
+    if (ws_bytes < need) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got %zu", need, ws_bytes);
+    if (!aligned(ws, 16)) return fail(KF_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
+  }
+  return hip_status(kf::gemm_launch(plan, x, packed, scales, y, ws, M, N, K, group_size,
+                                    static_cast<hipStream_t>(stream)),
+                    "int4_gemm launch");
+}
+
+int kf_int4_dequant_fp16(const void* packed, const void* scales, void* w_hat, int N, int K, int group_size,
+                         void* stream) {
+  if (!packed || !scales || !w_hat) return fail(KF_ERR_INVALID_ARG, "packed, scales and w_hat must be non-null");
+  if (N < 1 || K < 1) return fail(KF_ERR_INVALID_ARG, "N, K must be positive, got N=%d K=%d", N, K);
+  if (group_size != 64 && group_size != 128)
+    return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);
+  if (K % group_size != 0)
+    return fail(KF_ERR_INVALID_ARG, "K=%d is not a multiple of group_size=%d", K, group_size);
+  if (!aligned(packed, 4) || !aligned(scales, 2) || !aligned(w_hat, 16))
+    return fail(KF_ERR_INVALID_ARG, "packed must be 4-byte, scales 2-byte and w_hat 16-byte aligned");
+  return hip_status(kf::dequant_fp16_launch(packed, scales, w_hat, N, K, group_size,
+                                            static_cast<hipStream_t>(stream)),
+                    "dequant_fp16 launch");
+}
+
+static int bw_args(const void* a, size_t bytes, int* grid) {
+  if (!a) return fail(KF_ERR_INVALID_ARG, "buffer must be non-null");
+  if (bytes == 0 || bytes % 16) return fail(KF_ERR_INVALID_ARG, "bytes must be a positive multiple of 16");
+  if (!aligned(a, 16)) return fail(KF_ERR_INVALID_ARG, "buffers must be 16-byte aligned");
+  if (*grid <= 0) {
+    int cus = 0;
+    int st = cu_count(&cus);
+    if (st) return st;
+    *grid = 8 * cus;
+  }
+  return KF_OK;
+}
+
+int kf_bw_copy(const void* src, void* dst, size_t bytes, int grid_blocks, void* stream) {
+  int st = bw_args(src, bytes, &grid_blocks);
+  if (st) return st;
+  if (!dst || !aligned(dst, 16)) return fail(KF_ERR_INVALID_ARG, "dst must be non-null and 16-byte aligned");
+  return hip_status(kf::bw_copy_launch(src, dst, bytes, grid_blocks, static_cast<hipStream_t>(stream)), "bw_copy");
+}
+
+int kf_bw_read(const void* src, void* sink, size_t bytes, int grid_blocks, void* stream) {
+  int st = bw_args(src, bytes, &grid_blocks);
+  if (st) return st;
+  if (!sink) return fail(KF_ERR_INVALID_ARG, "sink must be non-null (4 bytes per block)");
+  return hip_status(kf::bw_read_launch(src, sink, bytes, grid_blocks, static_cast<hipStream_t>(stream)), "bw_read");
+}
+
+int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream) {
+  int st = bw_args(dst, bytes, &grid_blocks);
+  if (st) return st;
+  return hip_status(kf::bw_write_launch(dst, bytes, grid_blocks, static_cast<hipStream_t>(stream)), "bw_write");
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+// Auxiliary kernels: the fp16 dequantization exported for bit-exactness checks
+// and the streaming HBM ceiling kernels the roofline fractions are quoted against.
+#include "kf_device.h"
+#include "kf_launch.h"
+
+namespace kf {
+namespace {
+
+// One thread per packed word: the 8 weights of word i become fp16_rne(q * s),
+// using the same dequant8 the GEMM uses to fill its LDS tiles.
+__global__ __launch_bounds__(256) void dequant_fp16_kernel(const uint32_t* __restrict__ packed,
+                                                            const half_t* __restrict__ scales,
+                                                            half_t* __restrict__ out, size_t total_words,
+                                                            int words_per_row, int groups_per_row,
+                                                            int log2_group) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total_words; i += (size_t)gridDim.x * 256) {
+    const size_t n = i / words_per_row;
+    const int k0 = (int)(i - n * words_per_row) * 8;
+    const half_t s = scales[n * groups_per_row + (k0 >> log2_group)];
+    const half2_t s2 = {s, s};
+    *reinterpret_cast<half8_t*>(out + 8 * i) = dequant8(packed[i], s2);
+  }
+}
+
+__global__ __launch_bounds__(256) void bw_copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                       size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// Folds everything it reads into one word per thread; the store is taken only
+// when that word equals an unlikely constant, so the loads cannot be removed
+// but almost nothing is written.
+__global__ __launch_bounds__(256) void bw_read_kernel(const u32x4* __restrict__ src, uint32_t* __restrict__ sink,
+                                                       size_t n) {
+  uint32_t acc = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const u32x4 v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(256) void bw_write_kernel(u32x4* __restrict__ dst, size_t n) {
+  const u32x4 v = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    __builtin_nontemporal_store(v, dst + i);
+}
+
+}  // namespace
+
+hipError_t dequant_fp16_launch(const void* packed, const void* scales, void* w_hat, int N, int K, int group_size,
+                               hipStream_t stream) {
+  const size_t total = (size_t)N * (K / 8);
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL(dequant_fp16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(packed), static_cast<const half_t*>(scales),
+                     static_cast<half_t*>(w_hat), total, K / 8, K / group_size, group_size == 128 ? 7 : 6);
+  return hipGetLastError();
+}
+
+hipError_t bw_copy_launch(const void* src, void* dst, size_t bytes, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(bw_copy_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(src),
+                     static_cast<u32x4*>(dst), bytes / 16);
+  return hipGetLastError();
+}
+
+hipError_t bw_read_launch(const void* src, void* sink, size_t bytes, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(bw_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(src),
+                     static_cast<uint32_t*>(sink), bytes / 16);
+  return hipGetLastError();
+}
+
+hipError_t bw_write_launch(void* dst, size_t bytes, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(bw_write_kernel, dim3(grid), dim3(256), 0, stream, static_cast<u32x4*>(dst), bytes / 16);
+  return hipGetLastError();
+}
+
+}  // namespace kf

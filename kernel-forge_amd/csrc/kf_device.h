@@ -1,0 +1,81 @@
+// Device-side building blocks shared by the gfx950 INT4 kernels.
+//
+// Nibble unpack.  The packing convention (reference kernelforge/quantize.py:12-24)
+// stores k offsets (0,2,4,6,1,3,5,7) at nibble positions 0..7, so
+// (w >> 4i) & 0x000F000F holds u(k 2i) in bits 0-3 and u(k 2i+1) in bits 16-19.
+// OR-ing 0x6400 into each 16-bit half forms the fp16 number 1024 + u exactly
+// (fp16 spacing is 1 on [1024, 2048)), and one packed fp16 subtraction of
+// 1032 = 1024 + 8 yields (q[2i], q[2i+1]) exactly.  On gfx950 this is one
+// v_and_or_b32 and one v_pk_add_f16 per pair (plus a shift for i > 0).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kf {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename To, typename From>
+__device__ __forceinline__ To bit_cast(const From& v) {
+  static_assert(sizeof(To) == sizeof(From), "bit_cast size mismatch");
+  return __builtin_bit_cast(To, v);
+}
+
+// q pair (k 2i, k 2i+1) of a packed word as exact fp16 integers.
+template <int I>
+__device__ __forceinline__ half2_t nibble_pair(uint32_t w) {
+  const uint32_t v = ((w >> (4 * I)) & 0x000F000Fu) | 0x64006400u;
+  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  return bit_cast<half2_t>(v) - bias;
+}
+
+// All 8 weights of a word as fp16 integers in k order: (k0,k1),(k2,k3),(k4,k5),(k6,k7).
+__device__ __forceinline__ void unpack8(uint32_t w, half2_t (&q)[4]) {
+  q[0] = nibble_pair<0>(w);
+  q[1] = nibble_pair<1>(w);
+  q[2] = nibble_pair<2>(w);
+  q[3] = nibble_pair<3>(w);
+}
+
+// fp16_rne(q * s) for the 8 weights of a word: the dequantized W_hat the
+// reference feeds to its tensor cores (dequant_gemm_tc_kernel.cuh:100-112,
+// quantize.py:112-113).  q * s is exact before the single rounding because
+// |q| <= 8 has at most 4 significant bits.
+__device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
+  half2_t q[4];
+  unpack8(w, q);
+  const half2_t p0 = q[0] * s2, p1 = q[1] * s2, p2 = q[2] * s2, p3 = q[3] * s2;
+  half8_t out = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+  return out;
+}
+
+// Wave64 sum with DPP row ops; the total lands in lane 63.
+//   quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum
+//   row_shr:4, row_shr:8: lane 15 of each 16-lane row holds the row sum
+//   row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3: lane 63 holds the total
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
+__device__ __forceinline__ u32x4 load_u32x4(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Streaming (non-temporal) 16-byte load for data read exactly once.
+__device__ __forceinline__ u32x4 load_u32x4_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+}  // namespace kf

@@ -1,0 +1,77 @@
+"""ctypes binding of libkf_int4.so, the gfx950 HIP library behind kernelforge.ops.
+
+The library exports a plain C ABI (include/kf_int4.h).  This module loads it
+from the package directory, declares the signatures, and turns non-zero
+status codes into Python exceptions.  There is no fallback: if the library is
+missing or cannot be loaded, every op raises ImportError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libkf_int4.so")
+ABI_VERSION = 1
+
+KF_OK = 0
+KF_ERR_INVALID_ARG = 1
+KF_ERR_UNSUPPORTED = 2
+KF_ERR_WORKSPACE = 3
+KF_ERR_HIP = 4
+
+# Every symbol include/kf_int4.h declares, with (restype, argtypes).
+_VP, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+SIGNATURES = {
+    "kf_abi_version": (_I, []),
+    "kf_last_error": (ctypes.c_char_p, []),
+    "kf_int4_gemv": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
+    "kf_int4_dequant_fp16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "kf_bw_copy": (_I, [_VP, _VP, _SZ, _I, _VP]),
+    "kf_bw_read": (_I, [_VP, _VP, _SZ, _I, _VP]),
+    "kf_bw_write": (_I, [_VP, _SZ, _I, _VP]),
+}
+
+_lib: ctypes.CDLL | None = None
+_load_error: Exception | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads and type-annotates the library once; raises ImportError if it is unavailable."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH.name} is not built (expected at {LIB_PATH}). "
+                          "Build it with `python kernel-forge_amd/kernelforge/build.py` (hipcc, gfx950).")
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:  # missing HIP runtime, wrong architecture, ...
+        _load_error = exc
+        raise ImportError(f"cannot load {LIB_PATH}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.kf_abi_version()
+    if version != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH.name} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().kf_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(status: int, what: str) -> None:
+    """Raises for a non-zero status: ValueError for argument errors, RuntimeError otherwise."""
+    if status == KF_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if status in (KF_ERR_INVALID_ARG, KF_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(msg)

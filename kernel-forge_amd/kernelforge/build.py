@@ -1,0 +1,79 @@
+"""Builds libkf_int4.so in-tree for gfx950 with hipcc.
+
+    python -m kernelforge.build            # from kernel-forge_amd/
+    python kernel-forge_amd/kernelforge/build.py
+
+Each .hip translation unit is compiled to an object in parallel, then linked
+into ``kernelforge/libkf_int4.so``, where ``kernelforge._lib`` loads it.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+SRC_DIR = PKG_DIR.parent / "csrc"
+REPO_ROOT = PKG_DIR.parent.parent
+INCLUDE_DIR = REPO_ROOT / "include"
+BUILD_DIR = PKG_DIR.parent / "_build"
+LIB_NAME = "libkf_int4.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ARCH = "gfx950"
+
+SOURCES = ("kf_abi.hip", "kf_gemv.hip", "kf_gemm.hip", "kf_aux.hip")
+
+# Packed fp32 VALU ops stay disabled: the kernels never need them and some of
+# their forms are not trusted on the target machines.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the MI355X library needs ROCm's hipcc to build")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that noise.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build_library(verbose: bool = False, resource_usage: bool = False) -> Path:
+    """Compiles every kernel source and links libkf_int4.so; returns its path."""
+    cc = hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if resource_usage else []
+
+    def compile_one(src: str) -> Path:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        cmd = [cc, *COMMON_FLAGS, *DEVICE_FLAGS, *extra, "-I", str(INCLUDE_DIR), "-I", str(SRC_DIR),
+               "-c", str(SRC_DIR / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd))
+        _run(cmd)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 4)) as pool:
+        objs = list(pool.map(compile_one, SOURCES))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build_library(verbose="-v" in sys.argv, resource_usage="--resource-usage" in sys.argv)
+    print(f"built {path}")

@@ -1,0 +1,174 @@
+"""Python entry points of the MI355X INT4 weight-only linear path.
+
+Drop-in for the int4 part of the reference's ``kernelforge/ops.py``
+(:171-214, :277-302): same function names, signatures, defaults, validation
+order, exception types and messages, and the same
+``torch.library.custom_op("kernelforge::int4_matmul")`` with a fake impl.
+Underneath, every op calls the C ABI of ``libkf_int4.so`` (gfx950 HIP
+kernels) on torch's current HIP stream; outputs and split-K workspaces come
+from torch's caching allocator, so the ops are hipGraph-capturable.
+
+Inference only: no backward formulas are registered.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from kernelforge import _lib
+
+# Measured GEMV/GEMM crossover on one MI355X: the largest M at which the sum of
+# GEMV times over the layer shapes beats the GEMM's (reference rule,
+# bench/sweep_int4_dispatch.py:51-57).
+GEMV_MAX_M = 8
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _check_int4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> None:
+    """Reference kernelforge/ops.py:171-182 (same order, types and messages)."""
+    if not isinstance(x, torch.Tensor) or not x.is_cuda or x.dtype != torch.float16 or x.dim() != 2:
+        raise TypeError("x must be a 2-D fp16 CUDA tensor [M, K]")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous")
+    if packed.dtype != torch.int32 or scales.dtype != torch.float16:
+        raise TypeError("packed must be int32 and scales fp16 (see kernelforge.quantize)")
+    k = x.shape[1]
+    if k % group_size != 0:
+        raise ValueError(f"K={k} is not a multiple of group_size={group_size}")
+    if packed.shape[1] * 8 != k:
+        raise ValueError(f"packed has K/8={packed.shape[1]} columns but x has K={k}")
+
+
+def _check_native(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> None:
+    """Tensor checks the reference makes in C++ (csrc/gemm/dequant_gemv.cu:5-19); RuntimeError like TORCH_CHECK."""
+    for name, t in (("x", x), ("packed", packed), ("scales", scales)):
+        if not t.is_cuda:
+            raise RuntimeError(f"{name} must be a CUDA tensor")
+        if not t.is_contiguous():
+            raise RuntimeError(f"{name} must be contiguous")
+        if t.device != x.device:
+            raise RuntimeError(f"{name} is on {t.device} but x is on {x.device}")
+    if packed.dim() != 2:
+        raise RuntimeError("packed must be int32 [N, K / 8]")
+    if scales.dim() != 2:
+        raise RuntimeError("scales must be fp16 [N, K / group]")
+    if group_size not in (64, 128):
+        raise RuntimeError(f"group size must be 64 or 128, got {group_size}")
+    k, n = x.shape[1], packed.shape[0]
+    if scales.shape[0] != n or scales.shape[1] != k // group_size:
+        raise RuntimeError("scales must be [N, K / group]")
+    if x.data_ptr() % 16 or packed.data_ptr() % 16:
+        raise RuntimeError("INT4 kernels need 16-byte aligned inputs")
+
+
+def int4_gemv(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Fused INT4 dequant GEMV for M in [1, 8]: x [M, K] fp16 @ W_hat^T -> [M, N] fp16.
+
+    Reference kernelforge/ops.py:185-190; kernel csrc/kf_gemv.hip.
+    """
+    _check_int4(x, packed, scales, group_size)
+    if not 1 <= x.shape[0] <= 8:
+        raise ValueError(f"int4_gemv handles M in [1, 8], got M={x.shape[0]}")
+    _check_native(x, packed, scales, group_size)
+    lib = _lib.load()
+    m, k = x.shape
+    n = packed.shape[0]
+    y = torch.empty(m, n, dtype=torch.float16, device=x.device)
+    with torch.cuda.device(x.device):
+        status = lib.kf_int4_gemv(_ptr(x), _ptr(packed), _ptr(scales), _ptr(y), m, n, k, int(group_size),
+                                  _stream_ptr(x.device))
+    _lib.check(status, "int4_gemv")
+    return y
+
+
+def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Fused INT4 dequant GEMM on the MFMA matrix cores, any M, N a multiple of 64.
+
+    Reference kernelforge/ops.py:196-201; kernel csrc/kf_gemm.hip.
+    """
+    _check_int4(x, packed, scales, group_size)
+    if packed.shape[0] % 64 != 0:
+        raise ValueError(f"int4_gemm needs N to be a multiple of 64, got N={packed.shape[0]}")
+    _check_native(x, packed, scales, group_size)
+    lib = _lib.load()
+    m, k = x.shape
+    n = packed.shape[0]
+    y = torch.empty(m, n, dtype=torch.float16, device=x.device)
+    with torch.cuda.device(x.device):
+        ws_bytes = lib.kf_int4_gemm_workspace_bytes(m, n, k, int(group_size))
+        ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=x.device) if ws_bytes else None
+        status = lib.kf_int4_gemm(_ptr(x), _ptr(packed), _ptr(scales), _ptr(y),
+                                  _ptr(ws) if ws is not None else None, ws_bytes, m, n, k, int(group_size),
+                                  _stream_ptr(x.device))
+    _lib.check(status, "int4_gemm")
+    return y
+
+
+def int4_matmul(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """y = x @ W_hat^T for INT4 weights from kernelforge.quantize, choosing the kernel by M.
+
+    M <= GEMV_MAX_M: the bandwidth-bound GEMV; larger M: the MFMA GEMM.
+    Reference kernelforge/ops.py:204-214.
+    """
+    if x.shape[0] <= GEMV_MAX_M:
+        return int4_gemv(x, packed, scales, group_size)
+    return int4_gemm(x, packed, scales, group_size)
+
+
+def int4_dequant_fp16(packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """W_hat = fp16(q * s) [N, K] on the GPU, the exact operand the GEMM feeds to the matrix cores.
+
+    Counterpart of the reference's ``quantize.dequantize(qw, torch.float16)``
+    (kernelforge/quantize.py:108-113), exported for bit-exactness checks.
+    """
+    if packed.dtype != torch.int32 or scales.dtype != torch.float16:
+        raise TypeError("packed must be int32 and scales fp16 (see kernelforge.quantize)")
+    if not packed.is_cuda or not scales.is_cuda:
+        raise TypeError("packed and scales must be CUDA tensors")
+    if not packed.is_contiguous() or not scales.is_contiguous():
+        raise ValueError("packed and scales must be contiguous")
+    n, k = packed.shape[0], packed.shape[1] * 8
+    if scales.shape != (n, k // group_size):
+        raise ValueError("scales must be [N, K / group]")
+    lib = _lib.load()
+    w_hat = torch.empty(n, k, dtype=torch.float16, device=packed.device)
+    with torch.cuda.device(packed.device):
+        status = lib.kf_int4_dequant_fp16(_ptr(packed), _ptr(scales), _ptr(w_hat), n, k, int(group_size),
+                                          _stream_ptr(packed.device))
+    _lib.check(status, "int4_dequant_fp16")
+    return w_hat
+
+
+@torch.library.custom_op("kernelforge::int4_matmul", mutates_args=())
+def _int4_matmul_op(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    return int4_matmul(x, packed, scales, group_size)
+
+
+@_int4_matmul_op.register_fake
+def _(x, packed, scales, group_size):
+    return x.new_empty(x.shape[0], packed.shape[0])
+
+
+def int4_linear(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128,
+                bias: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ W_hat^T (+ bias) for INT4 weights from kernelforge.quantize. x: [..., K] fp16.
+
+    Leading dimensions are flattened into M like nn.Linear; the bias add is a
+    separate fp16 add, as in the reference (kernelforge/ops.py:287-302).
+    """
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    _check_int4(x2, packed, scales, group_size)
+    y = _int4_matmul_op(x2, packed, scales, int(group_size))
+    if bias is not None:
+        y = y + bias
+    return y.reshape(*lead, packed.shape[0])

@@ -1,0 +1,60 @@
+"""The C-ABI library: it loads, exports exactly what include/kf_int4.h declares,
+and rejects bad arguments before any GPU work (no compute calls here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernelforge import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kf_int4.h"
+
+
+def _declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(kf_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == set(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.kf_abi_version() == _lib.ABI_VERSION
+
+
+def _err(status, match):
+    assert status != 0
+    assert re.search(match, _lib.last_error()), _lib.last_error()
+
+
+def test_gemv_argument_errors_without_gpu():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    _err(lib.kf_int4_gemv(None, p, p, p, 1, 64, 256, 128, None), "non-null")
+    _err(lib.kf_int4_gemv(p, p, p, p, 1, 64, 200, 128, None), "not a multiple of group_size")
+    _err(lib.kf_int4_gemv(p, p, p, p, 1, 64, 256, 32, None), "group_size")
+    _err(lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None), r"M in \[1, 8\]")
+    _err(lib.kf_int4_gemv(p, p, p, p, 0, 64, 256, 128, None), "positive")
+    _err(lib.kf_int4_gemv(ctypes.c_void_p(0x1002), p, p, p, 1, 64, 256, 128, None), "16-byte aligned")
+    with pytest.raises(ValueError, match=r"M in \[1, 8\]"):
+        _lib.check(lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None), "int4_gemv")
+
+
+def test_gemm_argument_errors_without_gpu():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    _err(lib.kf_int4_gemm(p, p, p, p, None, 0, 16, 100, 256, 128, None), "multiple of 64")
+    _err(lib.kf_int4_gemm(p, p, None, p, None, 0, 16, 128, 256, 128, None), "non-null")
+    _err(lib.kf_int4_gemm(p, p, p, p, None, 0, 16, 128, 320, 128, None), "not a multiple of group_size")
+    _err(lib.kf_int4_dequant_fp16(None, p, p, 4, 256, 128, None), "non-null")
+    _err(lib.kf_bw_copy(p, p, 17, 0, None), "multiple of 16")
+    assert lib.kf_int4_gemm_workspace_bytes(0, 64, 256, 128) == 0

@@ -1,0 +1,348 @@
+"""Parity of the gfx950 INT4 kernels with the CPU oracle (needs a GPU).
+
+Mirrors the reference's tests/test_gemm.py: every TinyLlama / Qwen2.5 layer
+shape at every GEMV M (1..8) and the GEMM's M grid, both group sizes, ragged
+N, the dispatcher, and the rejection messages.  The oracle is the pinned numpy
+restatement of ``x.float() @ dequantize(qw, float32).T``; the pass rule is the
+reference's ``max|out - ref| <= 2e-3 * max|ref|`` (tests/test_gemm.py:17,36-45),
+stricter than the 1e-2 the north star allows.  Inputs are seeded on the CPU
+(numpy PCG64), weights ~ 0.02 N(0,1) quantized by the oracle, x ~ N(0,1) fp16.
+Dequantization is checked bit for bit.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from kernelforge import _lib, ops
+from kernelforge import quantize as kq
+from oracle import c_oracle
+from oracle import int4_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 2e-3
+DEV = "cuda"
+GOLDEN = Path(__file__).resolve().parent / "golden" / "int4_cases.npz"
+
+LAYER_SHAPES = {
+    "tinyllama_qo": (2048, 2048), "tinyllama_kv": (256, 2048), "tinyllama_gate_up": (5632, 2048),
+    "tinyllama_down": (2048, 5632), "qwen_qo": (1536, 1536), "qwen_kv": (256, 1536),
+    "qwen_gate_up": (8960, 1536), "qwen_down": (1536, 8960),
+}
+
+
+@functools.lru_cache(maxsize=None)
+def _weights(n: int, k: int, g: int):
+    """Oracle-quantized weight for (N, K, G), seeded by the shape; host arrays and device tensors."""
+    rng = np.random.Generator(np.random.PCG64(n * 31 + k))
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    packed, scales = o.quantize_weight(w, g)
+    return packed, scales, torch.from_numpy(packed).to(DEV), torch.from_numpy(scales).to(DEV)
+
+
+def _x(m: int, k: int, seed: int) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+
+
+def _check(error_log, suite, fn, m, n, k, g, case):
+    packed, scales, dp, ds = _weights(n, k, g)
+    x = _x(m, k, m * 7 + n + k)
+    ref = o.linear_ref_fp32(x, packed, scales, g)
+    out = fn(torch.from_numpy(x).to(DEV), dp, ds, g)
+    assert out.shape == (m, n) and out.dtype == torch.float16
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), f"{case}: non-finite output"
+    err = o.max_rel_err(got, ref)
+    error_log.add(suite, case=case, shape=[m, n, k], group=g, max_rel_err=err, passed=err <= REL_TOL)
+    assert err <= REL_TOL, f"{case} M={m} G={g}: rel err {err:.3e}"
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GEMV (reference tests/test_gemm.py:48-79)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("layer", list(LAYER_SHAPES))
+def test_gemv_layer_shapes(error_log, layer, m, group):
+    n, k = LAYER_SHAPES[layer]
+    _check(error_log, "int4_gemv", ops.int4_gemv, m, n, k, group, layer)
+
+
+@pytest.mark.parametrize("n", [1, 7, 9, 129])
+def test_gemv_ragged_n(error_log, n):
+    _check(error_log, "int4_gemv", ops.int4_gemv, 3, n, 256, 128, f"ragged_n{n}")
+
+
+@pytest.mark.parametrize("k", [64, 128, 2112, 4160])
+def test_gemv_odd_chunk_counts(error_log, k):
+    """K whose 32-weight chunk count is not a multiple of 64 lanes (partial last pass)."""
+    _check(error_log, "int4_gemv", ops.int4_gemv, 2, 200, k, 64, f"k{k}")
+
+
+def test_gemv_rejects_k_not_multiple_of_group():
+    x = torch.randn(1, 200, device=DEV).half()
+    packed = torch.zeros(16, 25, dtype=torch.int32, device=DEV)
+    scales = torch.ones(16, 2, dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError, match="not a multiple of group_size"):
+        ops.int4_gemv(x, packed, scales, 128)
+
+
+def test_gemv_rejects_large_m():
+    _, _, dp, ds = _weights(64, 256, 128)
+    x = torch.randn(9, 256, device=DEV).half()
+    with pytest.raises(ValueError, match=r"M in \[1, 8\]"):
+        ops.int4_gemv(x, dp, ds, 128)
+
+
+def test_gemv_rejects_shape_mismatch():
+    _, _, dp, ds = _weights(64, 256, 128)
+    x = torch.randn(1, 256, device=DEV).half()
+    with pytest.raises(ValueError, match="K/8"):
+        ops.int4_gemv(x[:, :128].contiguous(), dp, ds, 128)
+
+
+def test_rejects_cpu_and_wrong_dtype():
+    _, _, dp, ds = _weights(64, 256, 128)
+    with pytest.raises(TypeError, match="fp16 CUDA"):
+        ops.int4_gemv(torch.randn(1, 256).half(), dp, ds, 128)
+    with pytest.raises(TypeError, match="int32"):
+        ops.int4_gemv(torch.randn(1, 256, device=DEV).half(), dp.float(), ds, 128)
+
+
+# ---------------------------------------------------------------------------
+# GEMM (reference tests/test_gemm.py:82-99)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("m", [1, 8, 9, 16, 17, 32, 64, 65, 128])
+@pytest.mark.parametrize("layer", list(LAYER_SHAPES))
+def test_gemm_layer_shapes(error_log, layer, m, group):
+    n, k = LAYER_SHAPES[layer]
+    _check(error_log, "int4_gemm", ops.int4_gemm, m, n, k, group, layer)
+
+
+@pytest.mark.parametrize("m", [200, 256, 512, 2048])
+@pytest.mark.parametrize("layer", ["tinyllama_gate_up", "tinyllama_down"])
+def test_gemm_crossover_sweep_sizes(error_log, layer, m):
+    """BASELINE config 4's large-M points at full size, including the M=2048 headline."""
+    n, k = LAYER_SHAPES[layer]
+    _check(error_log, "int4_gemm", ops.int4_gemm, m, n, k, 128, f"{layer}_large_m")
+
+
+@pytest.mark.parametrize("n", [64, 192, 320])
+def test_gemm_n_multiple_of_64_not_128(error_log, n):
+    _check(error_log, "int4_gemm", ops.int4_gemm, 37, n, 512, 64, f"n{n}")
+
+
+@pytest.mark.parametrize("m", [1, 8, 9, 128])
+def test_matmul_dispatcher(error_log, m):
+    _check(error_log, "int4_matmul", ops.int4_matmul, m, 2048, 2048, 128, "dispatch")
+
+
+def test_gemm_rejects_n_not_multiple_of_64():
+    _, _, dp, ds = _weights(100, 256, 128)
+    x = torch.randn(16, 256, device=DEV).half()
+    with pytest.raises(ValueError, match="multiple of 64"):
+        ops.int4_gemm(x, dp, ds, 128)
+
+
+def test_splitk_is_deterministic():
+    """Split-K partials are reduced in fixed order: repeated calls are bitwise identical."""
+    n, k = LAYER_SHAPES["tinyllama_gate_up"]
+    _, _, dp, ds = _weights(n, k, 128)
+    x = torch.from_numpy(_x(16, k, 99)).to(DEV)
+    ws = _lib.load().kf_int4_gemm_workspace_bytes(16, n, k, 128)
+    assert ws > 0, "expected a split-K plan at M=16"
+    outs = [ops.int4_gemm(x, dp, ds, 128) for _ in range(3)]
+    assert all(torch.equal(outs[0], o_) for o_ in outs[1:])
+
+
+# ---------------------------------------------------------------------------
+# Bit-exact dequantization and fixed fixtures
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("layer", ["tinyllama_gate_up", "qwen_down"])
+@pytest.mark.parametrize("group", [64, 128])
+def test_dequant_fp16_bit_exact(layer, group):
+    n, k = LAYER_SHAPES[layer]
+    packed, scales, dp, ds = _weights(n, k, group)
+    got = ops.int4_dequant_fp16(dp, ds, group).cpu().numpy().view(np.uint16)
+    want = o.dequantize_fp16(packed, scales, group).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_golden_fixtures_all_paths(error_log):
+    data = np.load(GOLDEN)
+    for name in sorted({k.split("__")[0] for k in data.files}):
+        g = int(data[f"{name}__g"])
+        x = torch.from_numpy(data[f"{name}__x"]).to(DEV)
+        dp = torch.from_numpy(data[f"{name}__packed"]).to(DEV)
+        ds = torch.from_numpy(data[f"{name}__scales"]).to(DEV)
+        ref = data[f"{name}__y_ref32"]
+        w16 = ops.int4_dequant_fp16(dp, ds, g).cpu().numpy()
+        assert np.array_equal(w16.view(np.uint16), data[f"{name}__w_hat16"].view(np.uint16)), name
+        fns = [ops.int4_gemv, ops.int4_matmul] + ([ops.int4_gemm] if dp.shape[0] % 64 == 0 else [])
+        for fn in fns:
+            got = fn(x, dp, ds, g).float().cpu().numpy()
+            err = o.max_rel_err(got, ref)
+            error_log.add("golden", case=f"{name}:{fn.__name__}", shape=list(ref.shape), group=g,
+                          max_rel_err=err, passed=err <= REL_TOL)
+            assert err <= REL_TOL, f"{name} {fn.__name__}: {err:.3e}"
+
+
+@pytest.mark.parametrize("group", [64, 128])
+def test_reference_lcg_workload(error_log, group):
+    """The reference's torch-free workload (sanitize_gemm.cu:31-95): N=128, K=1024, 4-way split-K,
+    double-precision reference, GEMV at M <= 8 and the GEMM at every M."""
+    q, scales, packed, xs = c_oracle.lcg_workload(group)
+    dp = torch.from_numpy(packed).to(DEV)
+    ds = torch.from_numpy(np.ascontiguousarray(scales)).to(DEV)
+    for m, x in xs.items():
+        ref = c_oracle.ref_f64(x, packed, scales, group)
+        xd = torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+        fns = ([ops.int4_gemv] if m <= 8 else []) + [ops.int4_gemm]
+        for fn in fns:
+            got = fn(xd, dp, ds, group).float().cpu().numpy()
+            err = o.max_rel_err(got, ref)
+            error_log.add("lcg", case=fn.__name__, shape=[m, 128, 1024], group=group, max_rel_err=err,
+                          passed=err <= REL_TOL)
+            assert err <= REL_TOL, f"{fn.__name__} M={m} G={group}: {err:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# Guard bands: no write outside y, every element of y written
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind,m,n,k", [("gemv", 3, 129, 256), ("gemv", 8, 2048, 5632), ("gemm", 65, 192, 512),
+                                        ("gemm", 17, 5632, 2048), ("gemm", 300, 2048, 5632)])
+def test_output_guard_bands(kind, m, n, k):
+    g = 128
+    packed, scales, dp, ds = _weights(n, k, g)
+    x = torch.from_numpy(_x(m, k, 5)).to(DEV)
+    guard = 4096
+    sentinel = torch.tensor(-12345.0, dtype=torch.float16)  # exactly representable, not a plausible output
+    buf = torch.full((guard + m * n + guard,), float(sentinel), dtype=torch.float16, device=DEV)
+    y_ptr = buf.data_ptr() + 2 * guard
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    if kind == "gemv":
+        st = lib.kf_int4_gemv(x.data_ptr(), dp.data_ptr(), ds.data_ptr(), y_ptr, m, n, k, g, stream)
+    else:
+        wsb = lib.kf_int4_gemm_workspace_bytes(m, n, k, g)
+        ws = torch.empty(max(wsb, 16) // 4 + 1, dtype=torch.float32, device=DEV)
+        st = lib.kf_int4_gemm(x.data_ptr(), dp.data_ptr(), ds.data_ptr(), y_ptr, ws.data_ptr(), wsb, m, n, k, g,
+                              stream)
+    _lib.check(st, kind)
+    host = buf.cpu()
+    assert (host[:guard] == sentinel).all() and (host[guard + m * n:] == sentinel).all(), "write outside y"
+    y = host[guard:guard + m * n].float().numpy().reshape(m, n)
+    assert not (y == float(sentinel)).any(), "unwritten output element"
+    assert o.max_rel_err(y, o.linear_ref_fp32(_x(m, k, 5), packed, scales, g)) <= REL_TOL
+
+
+# ---------------------------------------------------------------------------
+# int4_linear, modules, graph capture
+# ---------------------------------------------------------------------------
+
+def test_int4_linear_leading_dims_and_bias():
+    n, k = 256, 2048
+    packed, scales, dp, ds = _weights(n, k, 128)
+    for lead in [(1, 1), (2, 3), (4, 16)]:
+        x = _x(int(np.prod(lead)), k, 17).reshape(*lead, k)
+        bias = torch.linspace(-1, 1, n, dtype=torch.float16, device=DEV)
+        y = ops.int4_linear(torch.from_numpy(x).to(DEV), dp, ds, 128, bias)
+        assert y.shape == (*lead, n) and y.dtype == torch.float16
+        ref = o.linear_ref_fp32(x.reshape(-1, k), packed, scales, 128).reshape(*lead, n) + bias.float().cpu().numpy()
+        assert o.max_rel_err(y.float().cpu().numpy(), ref) <= REL_TOL
+
+
+def test_custom_op_registered_and_fake():
+    x = torch.from_numpy(_x(4, 256, 3)).to(DEV)
+    _, _, dp, ds = _weights(64, 256, 128)
+    y = torch.ops.kernelforge.int4_matmul(x, dp, ds, 128)
+    assert y.shape == (4, 64)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode() as mode:
+        fx = mode.from_tensor(x)
+        fy = torch.ops.kernelforge.int4_matmul(fx, mode.from_tensor(dp), mode.from_tensor(ds), 128)
+        assert tuple(fy.shape) == (4, 64) and fy.dtype == torch.float16
+
+
+def test_quantize_linears_swaps_decoder_linears():
+    from kernelforge.modules import KFLinearInt4, quantize_linears_
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj = torch.nn.Linear(256, 256, bias=False)
+            self.k_proj = torch.nn.Linear(256, 64, bias=True)
+            self.lm_head = torch.nn.Linear(256, 128, bias=False)
+
+    torch.manual_seed(0)
+    blk = Block().to(DEV).half()
+    w_k = blk.k_proj.weight.detach().float().cpu().numpy()
+    b_k = blk.k_proj.bias.detach().cpu()
+    assert quantize_linears_(blk, 128) == 2
+    assert isinstance(blk.q_proj, KFLinearInt4) and isinstance(blk.lm_head, torch.nn.Linear)
+    x = _x(2, 256, 1)
+    y = blk.k_proj(torch.from_numpy(x).to(DEV))
+    packed, scales = o.quantize_weight(w_k, 128)
+    ref = o.linear_ref_fp32(x, packed, scales, 128) + b_k.float().numpy()
+    assert o.max_rel_err(y.float().cpu().numpy(), ref) <= REL_TOL
+    with pytest.raises(TypeError, match="fp16"):
+        blk.q_proj(torch.randn(1, 256, device=DEV))
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 128])
+def test_hip_graph_capture_replays_match_eager(m):
+    """Capture int4_linear (GEMV or GEMM + split-K) in a graph; every replay equals eager bitwise."""
+    n, k = LAYER_SHAPES["tinyllama_gate_up"]
+    _, _, dp, ds = _weights(n, k, 128)
+    static_x = torch.from_numpy(_x(m, k, 23)).to(DEV)
+    eager = ops.int4_linear(static_x, dp, ds, 128)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.int4_linear(static_x, dp, ds, 128)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_y = ops.int4_linear(static_x, dp, ds, 128)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, eager), f"replay {i}"
+        ops.int4_linear(static_x, dp, ds, 128)  # eager work between replays
+        torch.cuda.synchronize()
+    new_x = torch.from_numpy(_x(m, k, 24)).to(DEV)
+    static_x.copy_(new_x)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static_y, ops.int4_linear(new_x, dp, ds, 128))
+
+
+def test_bandwidth_kernels_roundtrip():
+    lib = _lib.load()
+    nbytes = 64 << 20
+    src = torch.randint(0, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=DEV)
+    dst = torch.zeros_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.kf_bw_copy(src.data_ptr(), dst.data_ptr(), nbytes, 0, stream), "copy")
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=DEV)
+    _lib.check(lib.kf_bw_read(src.data_ptr(), sink.data_ptr(), nbytes, 0, stream), "read")
+    _lib.check(lib.kf_bw_write(dst.data_ptr(), nbytes, 0, stream), "write")
+    torch.cuda.synchronize()
+    assert (dst.view(torch.int16) == 0x3C00).all()
