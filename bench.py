@@ -85,8 +85,11 @@ class Timer:
         self.torch = torch
         self.cycles_per_ms = self._calibrate()
 
-    def _calibrate(self) -> float:
+    def _calibrate(self) -> float | None:
         torch = self.torch
+        if not hasattr(torch.cuda, "_sleep"):
+            log("torch.cuda._sleep unavailable: per-launch timing runs without a launch guard")
+            return None
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         cycles = 2_000_000
         torch.cuda._sleep(cycles)
@@ -103,7 +106,8 @@ class Timer:
         for b0 in range(0, len(fns), batch):
             chunk = fns[b0:b0 + batch]
             evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunk]
-            torch.cuda._sleep(int(guard_ms * self.cycles_per_ms))
+            if self.cycles_per_ms:
+                torch.cuda._sleep(int(guard_ms * self.cycles_per_ms))
             for (s, e), fn in zip(evs, chunk):
                 s.record()
                 fn()

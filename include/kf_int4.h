@@ -55,6 +55,30 @@ const char* kf_last_error(void);
 int kf_int4_gemv(const void* x, const void* packed, const void* scales, void* y,
                  int M, int N, int K, int group_size, void* stream);
 
+/* One problem of a grouped GEMV launch: y = x @ W_hat^T with x fp16 [M, K],
+ * packed int32 [N, K/8], scales fp16 [N, K/G], y fp16 [M, N]. */
+typedef struct kf_gemv_problem {
+  const void* x;
+  const void* packed;
+  const void* scales;
+  void* y;
+  int N;
+  int K;
+} kf_gemv_problem;
+
+#define KF_GEMV_MAX_GROUP 8
+
+/* Up to KF_GEMV_MAX_GROUP independent GEMVs (common M in [1, 8] and G) in
+ * ONE launch; each output equals what kf_int4_gemv computes for that problem,
+ * bit for bit.  The problems array is read on the host during the call (it
+ * is passed to the kernel by value), so it may live on the caller's stack.
+ * No reference counterpart as an entry point: it is the multi-problem launch
+ * of the reference's GEMV (csrc/gemm/dequant_gemv_kernel.cuh:38-142), for
+ * decode linears that are independent (q|k|v on one x, gate|up on one x, or
+ * separate layers), since on MI355X a launch's fixed cost (~1.5 us) exceeds
+ * the time to stream a whole small layer. */
+int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int group_size, void* stream);
+
 /* Bytes of fp32 split-K workspace kf_int4_gemm needs for this problem on the
  * current device (0 when the chosen plan has no split-K).
  * Replaces kf::gemm_tc::workspace_floats (dequant_gemm_tc_kernel.cuh:179-183),

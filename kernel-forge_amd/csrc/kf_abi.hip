@@ -9,21 +9,26 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <atomic>
 
 #include "kf_int4.h"
 #include "kf_launch.h"
 
+static_assert(KF_GEMV_MAX_GROUP == kf::kMaxGemvGroup, "header and kernels disagree on the group limit");
+
 namespace {
 
 thread_local char g_error[512] = "";
 
 int fail(int status, const char* fmt, ...) {
+  char buf[sizeof(g_error)];  // the message may quote the previous one
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
+  memcpy(g_error, buf, sizeof(g_error));
   return status;
 }
 
@@ -84,10 +89,36 @@ int kf_int4_gemv(const void* x, const void* packed, const void* scales, void* y,
   if (M > 8) return fail(KF_ERR_INVALID_ARG, "int4_gemv handles M in [1, 8], got M=%d", M);
   int cus = 0;
   if ((st = cu_count(&cus))) return st;
-  const kf::GemvPlan plan = kf::gemv_plan(M, N, K, cus);
-  return hip_status(kf::gemv_launch(plan, x, packed, scales, y, M, N, K, group_size,
-                                    static_cast<hipStream_t>(stream)),
+  const kf::GemvProblem prob = {x, packed, scales, y, N, K};
+  const kf::GemvPlan plan = kf::gemv_plan(M, &N, &K, 1, cus);
+  return hip_status(kf::gemv_launch(plan, &prob, 1, M, group_size, static_cast<hipStream_t>(stream)),
                     "int4_gemv launch");
+}
+
+int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int group_size, void* stream) {
+  if (!problems) return fail(KF_ERR_INVALID_ARG, "problems must be non-null");
+  if (count < 1 || count > KF_GEMV_MAX_GROUP)
+    return fail(KF_ERR_INVALID_ARG, "count must be in [1, %d], got %d", KF_GEMV_MAX_GROUP, count);
+  if (M < 1 || M > 8) return fail(KF_ERR_INVALID_ARG, "int4_gemv handles M in [1, 8], got M=%d", M);
+  kf::GemvProblem probs[KF_GEMV_MAX_GROUP];
+  int ns[KF_GEMV_MAX_GROUP], ks[KF_GEMV_MAX_GROUP];
+  long waves = 0;
+  for (int i = 0; i < count; ++i) {
+    const kf_gemv_problem& p = problems[i];
+    int st = check_common(p.x, p.packed, p.scales, p.y, M, p.N, p.K, group_size);
+    if (st) return fail(st, "problem %d: %s", i, kf_last_error());
+    probs[i] = {p.x, p.packed, p.scales, p.y, p.N, p.K};
+    ns[i] = p.N;
+    ks[i] = p.K;
+    waves += p.N;
+  }
+  if (waves > (1L << 30)) return fail(KF_ERR_UNSUPPORTED, "total rows %ld too large for one launch", waves);
+  int cus = 0;
+  int st = cu_count(&cus);
+  if (st) return st;
+  const kf::GemvPlan plan = kf::gemv_plan(M, ns, ks, count, cus);
+  return hip_status(kf::gemv_launch(plan, probs, count, M, group_size, static_cast<hipStream_t>(stream)),
+                    "int4_gemv_grouped launch");
 }
 
 size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size) {

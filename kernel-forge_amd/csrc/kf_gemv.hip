@@ -1,52 +1,193 @@
-// Fused INT4 dequant GEMV for decode (M in [1, 8]) on gfx950.
+// Fused INT4 dequant GEMV for decode (M in [1, 8]) on gfx950, single- or multi-problem.
 //
-// Computes y[m, n] = fp16( sum_c s[n, c/(G/32)] * sum_{k in chunk c} x[m, k] * q[n, k] )
-// with fp32 accumulation, the arithmetic of the reference's
-// dequant_gemv_kernel<M> (csrc/gemm/dequant_gemv_kernel.cuh:38-109): the scale
-// is applied once per 32-k chunk (32 divides G), so W_hat is never rounded.
+// y[m, n] = fp16( sum_c s[n, c/(G/32)] * sum_{k in chunk c} x[m, k] * q[n, k] ), fp32
+// accumulation: the arithmetic of the reference's dequant_gemv_kernel<M>
+// (csrc/gemm/dequant_gemv_kernel.cuh:38-109).  The scale is applied once per
+// 32-k chunk (32 divides G), so W_hat is never rounded to fp16 here.
+//
+// One launch serves up to kMaxGemvGroup independent problems (x_p, W_p, y_p,
+// N_p, K_p) with a common M and G; a plain GEMV is a group of one.  On MI355X
+// an empty launch already costs ~1.6 us, longer than streaming a 2 MB layer,
+// so independent decode linears should share a launch.
 //
 // Mapping (bandwidth-first, no LDS, no MFMA):
 //   * A "chunk" is 32 consecutive k of one row: 16 B of packed words (one
 //     dwordx4), 64 B of x and exactly one scale.
-//   * Each wavefront owns R consecutive output rows.  Lane l handles chunks
-//     l, l+64, l+128, ... of every one of its rows, so one wavefront-wide
-//     dwordx4 instruction streams 1 KiB of a row contiguously.
-//   * U chunk iterations (U*R dwordx4 weight loads per lane) are issued before
-//     any arithmetic so enough bytes are in flight to cover HBM latency.
-//     Out-of-range chunks are clamped to the row's last chunk (always in
-//     bounds) and masked out of the sum.
-//   * The q unpack is done once per (chunk, row) and reused for all M rows
-//     of x; x is re-read per m from L1/L2 (a few KiB shared by all waves).
-//   * Each lane accumulates M*R fp32 partials; a DPP wave reduction puts the
-//     totals in lane 63, which rounds to fp16 (RNE) and stores them.
-//   * Rows past N are clamped to row N-1 for loading and never stored.
+//   * Each wavefront owns R consecutive rows of one problem.  Lane l handles
+//     chunks l, l+64, ... of its rows, so a wavefront-wide dwordx4 streams
+//     1 KiB of a row contiguously.
+//   * A pass covers UU (1..4) consecutive 64-chunk blocks; UU is picked per
+//     pass from the chunks left in the row, so a K=5632 row is one pass of
+//     3 blocks and a K=2048 row one pass of 1, in the same launch.  Every load
+//     of a pass (UU*R weight dwordx4, UU*R scales, x of the first XM rows) is
+//     issued before any arithmetic: one memory round trip per pass.
+//   * Unpack without magic numbers: a word masked with 0x000F000F holds the
+//     nibble pair (k0, k1) as two fp16 subnormals u * 2^-24; masked with
+//     0x00F000F0 the pair (k2, k3) becomes u * 2^-20; the word shifted right
+//     by 8 gives (k4, k5) and (k6, k7) the same way.  v_dot2_f32_f16 on these
+//     (exact products, fp32 sums) yields sum u*x up to a power of two, and
+//     sum q*x = sum u*x - 8 * sum x, with sum x per chunk shared by all rows
+//     of the wave.  5 bit operations and 4 dot2 per 8 weights per x row.
+//   * A DPP wave reduction leaves the totals in lane 63, which rounds to
+//     fp16 (RNE) and stores them.  Rows past N_p are clamped to row N_p - 1
+//     for loading and never stored.
+#include <limits.h>
+
 #include "kf_device.h"
 #include "kf_launch.h"
 
 namespace kf {
 namespace {
 
-template <int M, int R, int U>
-__global__ __launch_bounds__(256) void gemv_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
-                                                   const half_t* __restrict__ scales, half_t* __restrict__ y,
-                                                   int N, int K, int scale_shift) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
-  const int row0 = (blockIdx.x * waves + wave) * R;
-  if (row0 >= N) return;
+// x rows prefetched with the weights; larger M reads x per m inside the pass.
+template <int M>
+struct XPrefetch {
+  static constexpr int value = M < 2 ? M : 2;
+};
 
-  const int chunks = K >> 5;               // 32-k chunks per row
-  const int words = K >> 3;                // packed words per row
-  const int groups = chunks >> scale_shift;  // scales per row
+// Sum of the 32 x values of a chunk (fp32).
+__device__ __forceinline__ float chunk_xsum(const u32x4 (&xv)[4]) {
+  const half2_t one = {(half_t)1.0f, (half_t)1.0f};
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(xv[j][0]), one, s0, false);
+    s1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(xv[j][1]), one, s1, false);
+    s0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(xv[j][2]), one, s0, false);
+    s1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(xv[j][3]), one, s1, false);
+  }
+  return s0 + s1;
+}
 
+// The four masked forms of each word of a chunk: nibble pairs as fp16 subnormals.
+struct ChunkNibbles {
+  uint32_t t[4][4];  // [word][pair slot]: slots 0,2 hold u * 2^-24, slots 1,3 hold u * 2^-20
+};
+
+__device__ __forceinline__ void split_chunk(const u32x4& wv, ChunkNibbles& nb) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = wv[j], w8 = w >> 8;
+    nb.t[j][0] = w & 0x000F000Fu;   // (k0, k1)
+    nb.t[j][1] = w & 0x00F000F0u;   // (k2, k3) * 16
+    nb.t[j][2] = w8 & 0x000F000Fu;  // (k4, k5)
+    nb.t[j][3] = w8 & 0x00F000F0u;  // (k6, k7) * 16
+  }
+}
+
+// sum_{k in chunk} q[k] * x[k] for one row and one x row, in fp32.
+__device__ __forceinline__ float chunk_dot(const ChunkNibbles& nb, const u32x4 (&xv)[4], float xsum) {
+  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][0]), bit_cast<half2_t>(xv[j][0]), a0, false);
+    b0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][1]), bit_cast<half2_t>(xv[j][1]), b0, false);
+    a1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][2]), bit_cast<half2_t>(xv[j][2]), a1, false);
+    b1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][3]), bit_cast<half2_t>(xv[j][3]), b1, false);
+  }
+  const float ux = fmaf(b0 + b1, 0.0625f, a0 + a1) * 16777216.0f;  // 2^24 * (A + B / 16) = sum u*x
+  return fmaf(-8.0f, xsum, ux);                                     // q = u - 8
+}
+
+template <int R>
+struct RowSet {
   const uint32_t* prow[R];
   const half_t* srow[R];
+  const half_t* x;
+  int K;
+  int chunks;
+  int scale_shift;
+};
+
+// One pass over UU consecutive 64-chunk blocks starting at chunk base cb (uniform).
+template <int M, int R, int UU>
+__device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane, float (&acc)[M][R]) {
+  constexpr int XM = XPrefetch<M>::value;
+  u32x4 wv[UU][R];
+  half_t sv[UU][R];
+  u32x4 xv[UU][XM][4];
+#pragma unroll
+  for (int u = 0; u < UU; ++u) {
+    // Clamped to the row's last chunk: always in bounds and one basic block
+    // for all loads; lanes past the end re-read one line and are masked below.
+    const int c = min(cb + lane + 64 * u, rs.chunks - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wv[u][r] = load_u32x4_stream(rs.prow[r] + 4 * c);
+      sv[u][r] = rs.srow[r][c >> rs.scale_shift];
+    }
+#pragma unroll
+    for (int m = 0; m < XM; ++m) {
+      const u32x4* xp = reinterpret_cast<const u32x4*>(rs.x + (size_t)m * rs.K + 32 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[u][m][j] = xp[j];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of the math
+#pragma unroll
+  for (int u = 0; u < UU; ++u) {
+    const int c = cb + lane + 64 * u;
+    if (c < rs.chunks) {
+      ChunkNibbles nb[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) split_chunk(wv[u][r], nb[r]);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        u32x4 xm[4];
+        if (m < XM) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xm[j] = xv[u][m < XM ? m : 0][j];
+        } else {
+          const u32x4* xp = reinterpret_cast<const u32x4*>(rs.x + (size_t)m * rs.K + 32 * c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xm[j] = xp[j];
+        }
+        const float xsum = chunk_xsum(xm);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = fmaf((float)sv[u][r], chunk_dot(nb[r], xm, xsum), acc[m][r]);
+      }
+    }
+  }
+}
+
+template <int M, int R, int UMAX>
+__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const GemvBatch batch) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gwave = blockIdx.x * kGemvWavesPerBlock + wave;
+
+  // Problem lookup (uniform per wave) from the header alone: it is the first
+  // 64 bytes of the kernel arguments, read in one scalar load (or preloaded
+  // into SGPRs where the firmware supports kernarg preloading).
+  typedef int hdr_t __attribute__((ext_vector_type(kGemvHdr)));
+  const hdr_t h = *reinterpret_cast<const hdr_t*>(batch.hdr);
+  const int count = h[0];
+  int p = 0, base = 0;
+#pragma unroll
+  for (int i = 1; i <= kMaxGemvGroup; ++i) {
+    const int wb = h[2 + i];
+    if (gwave >= wb) {
+      p = i;
+      base = wb;
+    }
+  }
+  if (p >= count) return;  // past the last problem's waves
+
+  const GemvProblem& pr = batch.prob[p];
+  RowSet<R> rs;
+  rs.x = static_cast<const half_t*>(pr.x);
+  rs.K = pr.K;
+  rs.chunks = pr.K >> 5;
+  rs.scale_shift = h[1];
+  const int N = pr.N;
+  const int row0 = (gwave - base) * R;
+  const int words = pr.K >> 3;
+  const int groups = rs.chunks >> rs.scale_shift;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int n = min(row0 + r, N - 1);
-    prow[r] = packed + (size_t)n * words;
-    srow[r] = scales + (size_t)n * groups;
+    rs.prow[r] = static_cast<const uint32_t*>(pr.packed) + (size_t)n * words;
+    rs.srow[r] = static_cast<const half_t*>(pr.scales) + (size_t)n * groups;
   }
 
   float acc[M][R];
@@ -55,51 +196,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const half_t* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-  for (int c0 = lane; c0 < chunks; c0 += 64 * U) {
-    u32x4 wv[U][R];
-    half_t sv[U][R];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = min(c0 + 64 * u, chunks - 1);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        wv[u][r] = load_u32x4_stream(prow[r] + 4 * c);
-        sv[u][r] = srow[r][c >> scale_shift];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + 64 * u;
-      if (c < chunks) {
-        half2_t q[R][16];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t w = wv[u][r][j];
-            q[r][4 * j + 0] = nibble_pair<0>(w);
-            q[r][4 * j + 1] = nibble_pair<1>(w);
-            q[r][4 * j + 2] = nibble_pair<2>(w);
-            q[r][4 * j + 3] = nibble_pair<3>(w);
-          }
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const u32x4* xp = reinterpret_cast<const u32x4*>(x + (size_t)m * K + 32 * c);
-          u32x4 xv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xv[j] = xp[j];
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            float part = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                part = __builtin_amdgcn_fdot2(q[r][4 * j + i], bit_cast<half2_t>(xv[j][i]), part, false);
-            acc[m][r] = fmaf((float)sv[u][r], part, acc[m][r]);
-          }
-        }
-      }
+  for (int cb = 0; cb < rs.chunks;) {
+    const int left = rs.chunks - cb;  // uniform
+    if (UMAX >= 4 && left > 192) {
+      gemv_pass<M, R, (UMAX >= 4 ? 4 : 1)>(rs, cb, lane, acc);
+      cb += 256;
+    } else if (UMAX >= 3 && left > 128) {
+      gemv_pass<M, R, (UMAX >= 3 ? 3 : 1)>(rs, cb, lane, acc);
+      cb += 192;
+    } else if (UMAX >= 2 && left > 64) {
+      gemv_pass<M, R, (UMAX >= 2 ? 2 : 1)>(rs, cb, lane, acc);
+      cb += 128;
+    } else {
+      gemv_pass<M, R, 1>(rs, cb, lane, acc);
+      cb += 64;
     }
   }
 
@@ -109,6 +219,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const half_t* __restrict__ x,
     for (int r = 0; r < R; ++r) acc[m][r] = wave_sum_lane63(acc[m][r]);
 
   if (lane == 63) {
+    half_t* y = static_cast<half_t*>(pr.y);
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -117,11 +228,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const half_t* __restrict__ x,
   }
 }
 
-typedef void (*GemvFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int);
-
-// Instantiated (R, U) shapes; the plan only ever picks one of these.
-constexpr int kRs[3] = {1, 2, 4};
-constexpr int kUs[4] = {1, 2, 3, 4};
+typedef void (*GemvFn)(const GemvBatch);
 
 template <int M, int R>
 GemvFn pick_u(int U) {
@@ -135,11 +242,7 @@ GemvFn pick_u(int U) {
 
 template <int M>
 GemvFn pick_r(int R, int U) {
-  switch (R) {
-    case 1: return pick_u<M, 1>(U);
-    case 2: return pick_u<M, 2>(U);
-    default: return pick_u<M, 4>(U);
-  }
+  return R == 1 ? pick_u<M, 1>(U) : pick_u<M, 2>(U);
 }
 
 GemvFn pick(int M, int R, int U) {
@@ -157,37 +260,51 @@ GemvFn pick(int M, int R, int U) {
 
 }  // namespace
 
-GemvPlan gemv_plan(int M, int N, int K, int cu_count) {
-  (void)kRs;
-  (void)kUs;
+GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   GemvPlan p;
-  const int chunks = K / 32;
-  const int passes_one = ceil_div(chunks, 64);  // chunk iterations per lane
-  // Keep every lane's weight loads of a row in one pass when registers allow.
-  const int u_max = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
-  p.unroll = passes_one < u_max ? passes_one : u_max;
-  // Rows per wave: as many as still leave >= 4 wavefronts per CU.
-  const int target_waves = 4 * (cu_count > 0 ? cu_count : 256);
-  p.rows_per_wave = 1;
-  if (M <= 4) {
-    if (ceil_div(N, 4) >= target_waves) p.rows_per_wave = 4;
-    else if (ceil_div(N, 2) >= target_waves) p.rows_per_wave = 2;
-  } else if (ceil_div(N, 2) >= target_waves) {
-    p.rows_per_wave = 2;
+  long rows = 0;
+  int max_chunks = 0;
+  for (int i = 0; i < count; ++i) {
+    rows += N[i];
+    if (K[i] / 32 > max_chunks) max_chunks = K[i] / 32;
   }
-  p.waves_per_block = 4;
+  // Largest pass (in 64-chunk blocks) a wave may issue at once; register
+  // pressure grows with M, so fewer blocks per pass for larger M.
+  const int blocks = ceil_div(max_chunks, 64);
+  const int u_max = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
+  p.unroll = blocks < u_max ? blocks : u_max;
+  // Two rows per wave once that still leaves >= 8 wavefronts per CU.
+  const long target_waves = 8L * (cu_count > 0 ? cu_count : 256);
+  p.rows_per_wave = (rows + 1) / 2 >= target_waves ? 2 : 1;
   return p;
 }
 
-hipError_t gemv_launch(const GemvPlan& p, const void* x, const void* packed, const void* scales, void* y,
-                       int M, int N, int K, int group_size, hipStream_t stream) {
-  const int scale_shift = group_size == 128 ? 2 : 1;  // chunks per group = G / 32
-  const int waves = ceil_div(N, p.rows_per_wave);
-  const int blocks = ceil_div(waves, p.waves_per_block);
-  GemvFn fn = pick(M, p.rows_per_wave, p.unroll);
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * p.waves_per_block), 0, stream,
-                     static_cast<const half_t*>(x), static_cast<const uint32_t*>(packed),
-                     static_cast<const half_t*>(scales), static_cast<half_t*>(y), N, K, scale_shift);
+hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int count, int M, int group_size,
+                       hipStream_t stream) {
+  // Longest rows first: their waves carry the most bytes, so they are
+  // dispatched before the short ones (outputs do not depend on the order).
+  int order[kMaxGemvGroup];
+  for (int i = 0; i < count; ++i) order[i] = i;
+  for (int i = 1; i < count; ++i)
+    for (int j = i; j > 0 && problems[order[j]].K > problems[order[j - 1]].K; --j) {
+      const int t = order[j];
+      order[j] = order[j - 1];
+      order[j - 1] = t;
+    }
+  GemvBatch batch = {};
+  batch.hdr[0] = count;
+  batch.hdr[1] = group_size == 128 ? 2 : 1;  // log2(G / 32)
+  int waves = 0;
+  for (int i = 0; i < count; ++i) {
+    batch.prob[i] = problems[order[i]];
+    batch.hdr[2 + i] = waves;
+    waves += ceil_div(problems[order[i]].N, plan.rows_per_wave);
+  }
+  batch.hdr[2 + count] = waves;
+  for (int i = 3 + count; i < kGemvHdr; ++i) batch.hdr[i] = INT_MAX;
+  const int blocks = ceil_div(waves, kGemvWavesPerBlock);
+  hipLaunchKernelGGL(pick(M, plan.rows_per_wave, plan.unroll), dim3(blocks), dim3(64 * kGemvWavesPerBlock), 0,
+                     stream, batch);
   return hipGetLastError();
 }
 

@@ -10,15 +10,40 @@
 
 namespace kf {
 
-// ---- GEMV (M in [1, 8]) -------------------------------------------------
+// ---- GEMV (M in [1, 8]), one or several independent problems per launch ----
+constexpr int kMaxGemvGroup = 8;
+
+struct GemvProblem {
+  const void* x;       // fp16 [M, K]
+  const void* packed;  // int32 [N, K/8]
+  const void* scales;  // fp16 [N, K/G]
+  void* y;             // fp16 [M, N]
+  int N;
+  int K;
+};
+
+// Passed by value as the kernel argument (no device-side descriptor buffer).
+// hdr is read by each wavefront with a single 64-byte scalar load:
+//   hdr[0] = count, hdr[1] = log2(G / 32) (32-k chunks per scale group),
+//   hdr[2 + i] = first global wavefront of problem i (ascending), with
+//   hdr[2 + count] = total wavefronts and INT_MAX after it, so one comparison
+//   chain finds both the problem and whether the wave has any work.
+constexpr int kGemvHdr = 16;
+static_assert(kMaxGemvGroup + 4 <= kGemvHdr, "header too small for the group limit");
+struct GemvBatch {
+  int hdr[kGemvHdr];
+  GemvProblem prob[kMaxGemvGroup];
+};
+
+constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
+
 struct GemvPlan {
   int rows_per_wave;   // R: output rows one wavefront owns
   int unroll;          // U: 32-k chunks per lane kept in flight per pass
-  int waves_per_block; // W: wavefronts per workgroup
 };
-GemvPlan gemv_plan(int M, int N, int K, int cu_count);
-hipError_t gemv_launch(const GemvPlan& p, const void* x, const void* packed, const void* scales, void* y,
-                       int M, int N, int K, int group_size, hipStream_t stream);
+GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
+hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
+                       hipStream_t stream);
 
 // ---- MFMA GEMM (any M, N % 64 == 0) --------------------------------------
 struct GemmPlan {

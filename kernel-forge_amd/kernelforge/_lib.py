@@ -20,12 +20,23 @@ KF_ERR_UNSUPPORTED = 2
 KF_ERR_WORKSPACE = 3
 KF_ERR_HIP = 4
 
+GEMV_MAX_GROUP = 8
+
+
+class GemvProblem(ctypes.Structure):
+    """kf_gemv_problem of include/kf_int4.h."""
+
+    _fields_ = [("x", ctypes.c_void_p), ("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("N", ctypes.c_int), ("K", ctypes.c_int)]
+
+
 # Every symbol include/kf_int4.h declares, with (restype, argtypes).
 _VP, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 SIGNATURES = {
     "kf_abi_version": (_I, []),
     "kf_last_error": (ctypes.c_char_p, []),
     "kf_int4_gemv": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "kf_int4_gemv_grouped": (_I, [ctypes.POINTER(GemvProblem), _I, _I, _I, _VP]),
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
     "kf_int4_dequant_fp16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),

@@ -28,8 +28,12 @@ ARCH = "gfx950"
 SOURCES = ("kf_abi.hip", "kf_gemv.hip", "kf_gemm.hip", "kf_aux.hip")
 
 # Packed fp32 VALU ops stay disabled: the kernels never need them and some of
-# their forms are not trusted on the target machines.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# their forms are not trusted on the target machines.  The first 16 dwords of
+# kernel arguments are preloaded into SGPRs (gfx950 kernarg preloading; the
+# code object keeps a fallback prologue for firmware without it), which
+# removes a scalar memory round trip from the start of every wavefront.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-kernarg-preload-count=16"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result"]
 
 

@@ -146,6 +146,43 @@ def int4_dequant_fp16(packed: torch.Tensor, scales: torch.Tensor, group_size: in
     return w_hat
 
 
+def int4_gemv_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
+                      group_size: int = 128) -> list[torch.Tensor]:
+    """Several independent INT4 GEMVs (common M in [1, 8]) in one kernel launch per 8 problems.
+
+    Each output equals ``int4_gemv(xs[i], packed[i], scales[i], group_size)`` bit for bit.
+    This is the multi-problem launch of the GEMV (no reference counterpart as
+    an entry point): on MI355X a launch's fixed cost exceeds the time to stream
+    a small decode linear, so independent linears (q|k|v, gate|up, or separate
+    layers) should share a launch.  Kernel: csrc/kf_gemv.hip.
+    """
+    if not (len(xs) == len(packed) == len(scales)) or not xs:
+        raise ValueError("xs, packed and scales must be non-empty lists of equal length")
+    m = xs[0].shape[0] if isinstance(xs[0], torch.Tensor) and xs[0].dim() == 2 else -1
+    for x, p, s in zip(xs, packed, scales):
+        _check_int4(x, p, s, group_size)
+        if x.shape[0] != m:
+            raise ValueError(f"all problems must share M, got {x.shape[0]} and {m}")
+        if x.device != xs[0].device:
+            raise RuntimeError("all problems must be on one device")
+        _check_native(x, p, s, group_size)
+    if not 1 <= m <= 8:
+        raise ValueError(f"int4_gemv handles M in [1, 8], got M={m}")
+    lib = _lib.load()
+    dev = xs[0].device
+    ys = [torch.empty(m, p.shape[0], dtype=torch.float16, device=dev) for p in packed]
+    with torch.cuda.device(dev):
+        stream = _stream_ptr(dev)
+        for b0 in range(0, len(xs), _lib.GEMV_MAX_GROUP):
+            idx = range(b0, min(b0 + _lib.GEMV_MAX_GROUP, len(xs)))
+            probs = (_lib.GemvProblem * len(idx))(*[
+                _lib.GemvProblem(_ptr(xs[i]), _ptr(packed[i]), _ptr(scales[i]), _ptr(ys[i]),
+                                 packed[i].shape[0], xs[i].shape[1]) for i in idx])
+            status = lib.kf_int4_gemv_grouped(probs, len(idx), m, int(group_size), stream)
+            _lib.check(status, "int4_gemv_grouped")
+    return ys
+
+
 @torch.library.custom_op("kernelforge::int4_matmul", mutates_args=())
 def _int4_matmul_op(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
     return int4_matmul(x, packed, scales, group_size)
@@ -154,6 +191,41 @@ def _int4_matmul_op(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor,
 @_int4_matmul_op.register_fake
 def _(x, packed, scales, group_size):
     return x.new_empty(x.shape[0], packed.shape[0])
+
+
+@torch.library.custom_op("kernelforge::int4_matmul_grouped", mutates_args=())
+def _int4_matmul_grouped_op(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
+                            group_size: int) -> list[torch.Tensor]:
+    if xs[0].shape[0] <= GEMV_MAX_M:
+        return int4_gemv_grouped(xs, packed, scales, group_size)
+    return [int4_gemm(x, p, s, group_size) for x, p, s in zip(xs, packed, scales)]
+
+
+@_int4_matmul_grouped_op.register_fake
+def _(xs, packed, scales, group_size):
+    return [x.new_empty(x.shape[0], p.shape[0]) for x, p in zip(xs, packed)]
+
+
+def int4_linear_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
+                        group_size: int = 128, biases: list[torch.Tensor | None] | None = None
+                        ) -> list[torch.Tensor]:
+    """``[int4_linear(xs[i], packed[i], scales[i], group_size, biases[i]) ...]`` with one GEMV launch
+    for all problems at decode sizes (common flattened M <= GEMV_MAX_M); results are bit-identical."""
+    leads, flat = [], []
+    for x in xs:
+        leads.append(x.shape[:-1])
+        x2 = x.reshape(-1, x.shape[-1])
+        flat.append(x2 if x2.is_contiguous() else x2.contiguous())
+    for x2, p, s in zip(flat, packed, scales):
+        _check_int4(x2, p, s, group_size)
+    ys = _int4_matmul_grouped_op(flat, list(packed), list(scales), int(group_size))
+    out = []
+    for i, y in enumerate(ys):
+        b = biases[i] if biases is not None else None
+        if b is not None:
+            y = y + b
+        out.append(y.reshape(*leads[i], packed[i].shape[0]))
+    return out
 
 
 def int4_linear(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128,

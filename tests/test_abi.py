@@ -49,6 +49,19 @@ def test_gemv_argument_errors_without_gpu():
         _lib.check(lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None), "int4_gemv")
 
 
+def test_grouped_gemv_argument_errors_without_gpu():
+    lib = _lib.load()
+    good = _lib.GemvProblem(0x1000, 0x1000, 0x1000, 0x1000, 64, 256)
+    bad_k = _lib.GemvProblem(0x1000, 0x1000, 0x1000, 0x1000, 64, 200)
+    arr = (_lib.GemvProblem * 9)(*([good] * 9))
+    _err(lib.kf_int4_gemv_grouped(None, 1, 1, 128, None), "non-null")
+    _err(lib.kf_int4_gemv_grouped(arr, 0, 1, 128, None), r"count must be in \[1, 8\]")
+    _err(lib.kf_int4_gemv_grouped(arr, 9, 1, 128, None), r"count must be in \[1, 8\]")
+    _err(lib.kf_int4_gemv_grouped(arr, 2, 9, 128, None), r"M in \[1, 8\]")
+    mixed = (_lib.GemvProblem * 2)(good, bad_k)
+    _err(lib.kf_int4_gemv_grouped(mixed, 2, 1, 128, None), "problem 1: K=200 is not a multiple of group_size")
+
+
 def test_gemm_argument_errors_without_gpu():
     lib = _lib.load()
     p = ctypes.c_void_p(0x1000)

@@ -120,6 +120,70 @@ def test_rejects_cpu_and_wrong_dtype():
 
 
 # ---------------------------------------------------------------------------
+# Multi-problem GEMV launch
+# ---------------------------------------------------------------------------
+
+TL_SEVEN = ["tinyllama_qo", "tinyllama_kv", "tinyllama_kv", "tinyllama_qo", "tinyllama_gate_up",
+            "tinyllama_gate_up", "tinyllama_down"]
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_gemv_bit_identical_to_single(error_log, m, group):
+    """All 7 TinyLlama linears (plus Qwen's down, > 8 problems -> two launches) in grouped launches:
+    each output equals the single-problem GEMV bit for bit and the oracle within tolerance."""
+    names = TL_SEVEN + ["qwen_down", "qwen_kv"]
+    xs, ps, ss, refs = [], [], [], []
+    for i, name in enumerate(names):
+        n, k = LAYER_SHAPES[name]
+        packed, scales, dp, ds = _weights(n, k, group)
+        x = _x(m, k, 1000 + i)
+        xs.append(torch.from_numpy(x).to(DEV))
+        ps.append(dp)
+        ss.append(ds)
+        refs.append(o.linear_ref_fp32(x, packed, scales, group))
+    ys = ops.int4_gemv_grouped(xs, ps, ss, group)
+    for i, name in enumerate(names):
+        single = ops.int4_gemv(xs[i], ps[i], ss[i], group)
+        assert torch.equal(ys[i], single), f"{name}: grouped differs from single"
+        err = o.max_rel_err(ys[i].float().cpu().numpy(), refs[i])
+        error_log.add("int4_gemv_grouped", case=name, shape=[m, *LAYER_SHAPES[name]], group=group,
+                      max_rel_err=err, passed=err <= REL_TOL)
+        assert err <= REL_TOL, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("shapes,m_leads", [
+    ([(9, 256), (129, 512), (64, 4160), (1, 128)], [(1, 1), (2, 3)]),  # ragged N: GEMV sizes only
+    ([(64, 256), (192, 512), (128, 4160)], [(2, 5), (33,)]),            # M > GEMV_MAX_M: per-problem GEMM
+])
+def test_grouped_linear_ragged_and_bias(shapes, m_leads):
+    """Ragged N, different K per problem, biases, 3-D inputs, and the large-M path."""
+    for m_lead in m_leads:
+        xs, ps, ss, bs, refs = [], [], [], [], []
+        for i, (n, k) in enumerate(shapes):
+            packed, scales, dp, ds = _weights(n, k, 64)
+            x = _x(int(np.prod(m_lead)), k, 50 + i)
+            xs.append(torch.from_numpy(x).to(DEV).reshape(*m_lead, k))
+            ps.append(dp)
+            ss.append(ds)
+            b = torch.randn(n, device=DEV).half() if i % 2 == 0 else None
+            bs.append(b)
+            ref = o.linear_ref_fp32(x, packed, scales, 64)
+            refs.append(ref + (b.float().cpu().numpy() if b is not None else 0))
+        ys = ops.int4_linear_grouped(xs, ps, ss, 64, bs)
+        for i, y in enumerate(ys):
+            assert y.shape == (*m_lead, shapes[i][0])
+            assert o.max_rel_err(y.float().cpu().numpy().reshape(refs[i].shape), refs[i]) <= REL_TOL
+
+
+def test_grouped_rejects_mixed_m():
+    _, _, dp, ds = _weights(64, 256, 128)
+    with pytest.raises(ValueError, match="share M"):
+        ops.int4_gemv_grouped([torch.randn(1, 256, device=DEV).half(), torch.randn(2, 256, device=DEV).half()],
+                              [dp, dp], [ds, ds], 128)
+
+
+# ---------------------------------------------------------------------------
 # GEMM (reference tests/test_gemm.py:82-99)
 # ---------------------------------------------------------------------------
 
