@@ -3,32 +3,39 @@
 
 Metric (BASELINE.json): "int4_linear M=1 HBM GB/s (% peak) over 7 layers; TFLOPS at M=2048".
 
-A *step* is one pass of the hot path over one batch: the 7 TinyLlama-1.1B
-decoder linears (q, k, v, o, gate, up, down; G=128) at M=1, each an
-``ops.int4_linear`` call.  ``value`` is the 7-layer
-algorithmic bytes (22,779,904 B; bench/bench_gemm.py:80,98) divided by the
-measured time per step, in GB/s.
+Workload: the 7 TinyLlama-1.1B decoder linears (q, k, v,
+o, gate, up, down; G=128) at M=1.  Weights W ~ 0.02 N(0,1) fp32 per layer
+(seeded) quantized by the package's quantize_weight, x ~ N(0,1) fp16 per
+layer: synthetic, resident in HBM.  A *step* computes all 7 linears once;
+``value`` = the 7-layer algorithmic bytes (22,779,904 B, formula of
+bench/bench_gemm.py:80,98) / time per step, in GB/s.
+
+The 7 problems of a step are independent, so the step is one
+``ops.int4_linear_grouped`` call: one GEMV launch over all 7 (each output is
+bit-identical to its own ``int4_linear``).  Two other step structures are
+timed and reported beside it:
+  * decoder: the launches a real decoder layer can make, where q|k|v share x
+    and gate|up share x: grouped(q,k,v), o, grouped(gate,up), down;
+  * separate: 7 ``ops.int4_linear`` calls, one launch each (the reference's
+    per-layer structure).
 
 Protocol
-* Weights: W ~ 0.02 N(0,1) fp32 per layer (seeded), quantized with the
-  package's quantize_weight; x ~ N(0,1) fp16.  Synthetic, resident in HBM.
 * Infinity-Cache-cold: R copies of the 7-layer weight set (R * 22.8 MB >= 2x
-  the 256 MB MALL) are rotated, step i using copy i % R, so no step finds its
-  weights in the MALL or L2.
-* The steps are captured in HIP graphs (R steps per graph), so host launch
-  cost is excluded as in the reference's CUDA-graph decode; W warm-up steps,
-  then exactly K timed steps bracketed by torch.cuda.synchronize().
-* roofline: the dominant kernel is the M=1 GEMV on the gate/up shape
-  (N=5632, K=2048, 5,962,752 B per launch).  Its average duration is measured
-  live with one HIP event pair per launch on the launching stream, launches
-  queued behind a GPU spin so only GPU time is inside each pair, MALL-cold.
+  the 256 MB MALL) are rotated, step i using copy i % R.
+* Steps are captured in HIP graphs (R steps per graph; host launch cost is
+  excluded, as in the reference's CUDA-graph decode); W warm-up steps, then
+  exactly K timed steps bracketed by torch.cuda.synchronize().
+* roofline: the dominant kernel is the grouped GEMV (the whole step).  Its
+  average duration per launch is measured live with a HIP event pair around
+  graph replays of back-to-back launches (rotating copies) on the launching
+  stream; achieved = 22,779,904 B / that duration.
 * ceilings: HBM copy/read peaks measured in the same run with the library's
-  dwordx4 kernels on 1 GiB buffers; fp16 MFMA peak measured with torch.matmul
+  dwordx4 kernels on 1 GiB buffers; fp16 MFMA peak with torch.matmul
   (hipBLASLt) at 4096/6144/8192.
-* M=2048: the GEMM on every TinyLlama shape at M=2048, event-timed; TFLOPS
-  (2*M*N*K / time) for gate and for the 7-layer sum.
+* M=2048 (BASELINE config 4's largest point): the MFMA GEMM on every
+  TinyLlama shape; TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum.
 * cpu_baseline: the oracle's FP32 dequant + matmul (numpy; the reference's
-  CPU path restated) on the host cores, over a bounded sample.
+  CPU path restated) on the host cores over a bounded sample.
 
 --gpus N > 1 is refused: this build measures one GPU.
 """
@@ -55,7 +62,7 @@ TL_LAYERS = [("q", 2048, 2048), ("k", 256, 2048), ("v", 256, 2048), ("o", 2048, 
 MALL_BYTES = 256 << 20
 SPEC_HBM_GBPS = 8000.0
 SPEC_FP16_TFLOPS = 2500.0
-REFERENCE_PCT_OF_COPY = 79.0  # reference's 7-layer aggregate on its own GPU
+REFERENCE_PCT_OF_COPY = 79.0  # reference's 7-layer aggregate on its own GPU (RTX 4060 Laptop)
 
 
 def algo_bytes(m: int, n: int, k: int, g: int = GROUP) -> int:
@@ -70,65 +77,118 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-m2048", action="store_true", help="skip the M=2048 GEMM leg")
-    ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "copy"],
+                    help="only launch one kernel --profile-iters times (for rocprofv3 --pmc runs) and exit")
+    ap.add_argument("--profile-iters", type=int, default=20)
     return ap.parse_args()
+
+
+def profile_only(args, torch, lib, kl, ops, kq) -> int:
+    """Launches one kernel a fixed number of times, eagerly, for counter collection.
+
+    gemv_grouped: the grouped 7-layer GEMV (22,779,904 algorithmic bytes per launch), rotating
+      weight copies so every launch reads its weights from HBM.
+    gemm_m2048:  the MFMA GEMM on the gate shape at M=2048.
+    copy:        kf_bw_copy of 64 MiB (64 MiB read + 64 MiB written per launch), the known-size
+      kernel that calibrates FETCH_SIZE / WRITE_SIZE.
+    """
+    stream = torch.cuda.current_stream().cuda_stream
+    if args.profile == "copy":
+        nbytes = 64 << 20
+        a = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(args.profile_iters):
+            kl.check(lib.kf_bw_copy(a.data_ptr(), b.data_ptr(), nbytes, 0, stream), "copy")
+    elif args.profile == "gemm_m2048":
+        layers = make_layers(torch, kq)
+        gate = [ly for ly in layers if ly["name"] == "gate"][0]
+        p, s = gate["packed"].cuda(), gate["scales"].cuda()
+        x = torch.randn(2048, gate["K"], dtype=torch.float16, device="cuda")
+        for _ in range(args.profile_iters):
+            ops.int4_gemm(x, p, s, GROUP)
+    else:
+        layers = make_layers(torch, kq)
+        set_bytes = sum(ly["packed"].numel() * 4 + ly["scales"].numel() * 2 for ly in layers)
+        copies = max(2, -(-(2 * MALL_BYTES) // set_bytes))
+        dev = [[(ly["packed"].cuda(), ly["scales"].cuda()) for ly in layers] for _ in range(copies)]
+        xs = [ly["x"].cuda() for ly in layers]
+        for i in range(args.profile_iters):
+            r = i % copies
+            ops.int4_linear_grouped(xs, [d[0] for d in dev[r]], [d[1] for d in dev[r]], GROUP)
+    torch.cuda.synchronize()
+    print(f"profiled {args.profile} x{args.profile_iters}", flush=True)
+    return 0
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-class Timer:
-    """Per-launch HIP event pairs, launches queued behind a GPU spin (reference bench_utils.py:114-185)."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    def __init__(self, torch):
-        self.torch = torch
-        self.cycles_per_ms = self._calibrate()
 
-    def _calibrate(self) -> float | None:
-        torch = self.torch
-        if not hasattr(torch.cuda, "_sleep"):
-            log("torch.cuda._sleep unavailable: per-launch timing runs without a launch guard")
-            return None
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        cycles = 2_000_000
-        torch.cuda._sleep(cycles)
+class GraphSteps:
+    """Runs `count` steps as replays of captured graphs; step i uses weight copy i % copies."""
+
+    def __init__(self, torch, step_fn, copies: int):
+        self.torch, self.step_fn, self.copies = torch, step_fn, copies
+        self.graphs = {}
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # eager warm-up off the capture path
+            for r in range(copies):
+                step_fn(r)
+        torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
+
+    def _graph(self, n: int):
+        if n not in self.graphs:
+            g = self.torch.cuda.CUDAGraph()
+            with self.torch.cuda.graph(g):
+                for r in range(n):
+                    self.step_fn(r)
+            self.graphs[n] = g
+        return self.graphs[n]
+
+    def run(self, count: int) -> None:
+        full, rem = divmod(count, self.copies)
+        for _ in range(full):
+            self._graph(self.copies).replay()
+        if rem:
+            self._graph(rem).replay()
+
+    def event_avg_ms(self, count: int) -> float:
+        """Average time per step from one HIP event pair on the launching stream."""
+        torch = self.torch
+        self.run(count)  # make sure every graph used below exists
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        torch.cuda._sleep(cycles)
+        self.run(count)
         e.record()
         torch.cuda.synchronize()
-        return cycles / max(s.elapsed_time(e), 1e-3)
-
-    def per_launch_ms(self, fns, batch: int = 16, guard_ms: float = 2.0) -> list[float]:
-        torch = self.torch
-        out = []
-        for b0 in range(0, len(fns), batch):
-            chunk = fns[b0:b0 + batch]
-            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunk]
-            if self.cycles_per_ms:
-                torch.cuda._sleep(int(guard_ms * self.cycles_per_ms))
-            for (s, e), fn in zip(evs, chunk):
-                s.record()
-                fn()
-                e.record()
-            torch.cuda.synchronize()
-            out += [s.elapsed_time(e) for s, e in evs]
-        return out
-
-    def batch_avg_ms(self, fn, reps: int) -> float:
-        torch = self.torch
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        s.record()
-        for _ in range(reps):
-            fn()
-        e.record()
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) / reps
+        return s.elapsed_time(e) / count
 
 
-def measure_hbm(torch, lib, kl, timer) -> dict:
+def batch_avg_ms(torch, fn, reps: int) -> float:
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def measure_hbm(torch, lib, kl) -> dict:
     """Copy and read ceilings over 1 GiB buffers (4x the MALL), best over grid sizes."""
     nbytes = 1 << 30
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
@@ -144,9 +204,10 @@ def measure_hbm(torch, lib, kl, timer) -> dict:
         def read():
             kl.check(lib.kf_bw_read(a.data_ptr(), sink.data_ptr(), nbytes, grid, stream), "read")
 
-        copy(), read()
-        t_copy = min(timer.batch_avg_ms(copy, 1) for _ in range(5))
-        t_read = min(timer.batch_avg_ms(read, 1) for _ in range(5))
+        copy()
+        read()
+        t_copy = min(batch_avg_ms(torch, copy, 1) for _ in range(5))
+        t_read = min(batch_avg_ms(torch, read, 1) for _ in range(5))
         best["copy"] = max(best["copy"], 2 * nbytes / (t_copy * 1e-3) / 1e9)
         best["read"] = max(best["read"], nbytes / (t_read * 1e-3) / 1e9)
     del a, b
@@ -154,13 +215,13 @@ def measure_hbm(torch, lib, kl, timer) -> dict:
     return {"hbm_copy_gbps": best["copy"], "hbm_read_gbps": best["read"], "buffer_bytes": nbytes}
 
 
-def measure_mfma_peak(torch, timer) -> float:
+def measure_mfma_peak(torch) -> float:
     best = 0.0
     for s in (4096, 6144, 8192):
         a = torch.randn(s, s, dtype=torch.float16, device="cuda")
         b = torch.randn(s, s, dtype=torch.float16, device="cuda")
         torch.matmul(a, b)
-        t = min(timer.batch_avg_ms(lambda: torch.matmul(a, b), 3) for _ in range(3))
+        t = min(batch_avg_ms(torch, lambda: torch.matmul(a, b), 3) for _ in range(3))
         best = max(best, 2 * s ** 3 / (t * 1e-3) / 1e12)
         del a, b
     torch.cuda.empty_cache()
@@ -175,7 +236,7 @@ def make_layers(torch, kq):
         w = torch.randn(n, k, generator=g) * 0.02
         qw = kq.quantize_weight(w, GROUP)
         x = torch.randn(1, k, generator=g).half()
-        layers.append((name, n, k, qw.packed, qw.scales, x))
+        layers.append({"name": name, "N": n, "K": k, "packed": qw.packed, "scales": qw.scales, "x": x})
     return layers
 
 
@@ -186,7 +247,6 @@ def main() -> int:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
               "This build has no multi-GPU path; run with --gpus 1.", file=sys.stderr)
         return 2
-    import numpy as np
     import torch
 
     from kernelforge import _lib as kl
@@ -199,114 +259,95 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     props = torch.cuda.get_device_properties(0)
-    timer = Timer(torch)
-    stream_ptr = torch.cuda.current_stream().cuda_stream
+    if args.profile:
+        return profile_only(args, torch, lib, kl, ops, kq)
 
     log("measuring HBM ceilings")
-    ceil = measure_hbm(torch, lib, kl, timer)
+    ceil = measure_hbm(torch, lib, kl)
     log(f"copy {ceil['hbm_copy_gbps']:.0f} GB/s, read {ceil['hbm_read_gbps']:.0f} GB/s")
 
     log("quantizing TinyLlama-shaped layers")
     layers = make_layers(torch, kq)
-    step_bytes = sum(algo_bytes(1, n, k) for _, n, k, *_ in layers)
-    set_bytes = sum(p.numel() * 4 + s.numel() * 2 for *_, p, s, _x in layers)
+    names = [ly["name"] for ly in layers]
+    idx = {nm: i for i, nm in enumerate(names)}
+    step_bytes = sum(algo_bytes(1, ly["N"], ly["K"]) for ly in layers)
+    set_bytes = sum(ly["packed"].numel() * 4 + ly["scales"].numel() * 2 for ly in layers)
     copies = max(2, -(-(2 * MALL_BYTES) // set_bytes))
-    dev_sets = [[(p.cuda(), s.cuda()) for *_, p, s, _x in layers] for _ in range(copies)]
-    xs = [x.cuda() for *_, x in layers]
+    dev = [[(ly["packed"].cuda(), ly["scales"].cuda()) for ly in layers] for _ in range(copies)]
+    xs = [ly["x"].cuda() for ly in layers]
 
-    # --- the timed step: 7 int4_linear calls, graph-captured, rotating weight copies ---------------
-    def run_step(r):
-        for li, (name, n, k, *_rest) in enumerate(layers):
-            p, s = dev_sets[r][li]
-            ops.int4_linear(xs[li], p, s, GROUP)
+    def grouped(r, subset):
+        ids = [idx[nm] for nm in subset]
+        return ops.int4_linear_grouped([xs[i] for i in ids], [dev[r][i][0] for i in ids],
+                                       [dev[r][i][1] for i in ids], GROUP)
 
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for r in range(copies):
-            run_step(r)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
+    def single(r, nm):
+        i = idx[nm]
+        return ops.int4_linear(xs[i], dev[r][i][0], dev[r][i][1], GROUP)
 
-    graphs = {}
+    def step_grouped(r):
+        grouped(r, names)
 
-    def graph_for(count):
-        if count not in graphs:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                for r in range(count):
-                    run_step(r)
-            graphs[count] = g
-        return graphs[count]
+    def step_decoder(r):
+        grouped(r, ["q", "k", "v"])
+        single(r, "o")
+        grouped(r, ["gate", "up"])
+        single(r, "down")
 
-    def run_steps(n_steps):
-        full, rem = divmod(n_steps, copies)
-        for _ in range(full):
-            graph_for(copies).replay()
-        if rem:
-            graph_for(rem).replay()
+    def step_separate(r):
+        for nm in names:
+            single(r, nm)
 
+    # --- the timed step (value): one grouped launch over the 7 linears --------------------------
     log(f"{copies} weight copies ({copies * set_bytes / 2**20:.0f} MiB); warmup {args.warmup} steps")
-    run_steps(args.warmup)
+    main_steps = GraphSteps(torch, step_grouped, copies)
+    main_steps.run(args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run_steps(args.steps)
+    main_steps.run(args.steps)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"7-layer step {ms_per_step * 1e3:.2f} us -> {value:.0f} GB/s")
+    log(f"grouped 7-layer step {ms_per_step * 1e3:.2f} us -> {value:.0f} GB/s")
 
-    # --- dominant kernel: M=1 GEMV on the gate shape, per-launch events, MALL-cold ----------------
-    gate_idx = [nm for nm, *_ in layers].index("gate")
-    _, gn, gk, *_ = layers[gate_idx]
-    y_gate = torch.empty(1, gn, dtype=torch.float16, device="cuda")
+    # --- roofline of the dominant kernel (the grouped GEMV: one launch per step) ----------------
+    gemv_avg_ms = main_steps.event_avg_ms(8 * copies)
+    achieved = step_bytes / (gemv_avg_ms * 1e-3) / 1e9
+    log(f"grouped GEMV avg {gemv_avg_ms * 1e3:.2f} us per launch -> {achieved:.0f} GB/s")
 
-    def gemv_launch(r, li=gate_idx, y=None):
-        _, n, k, *_r = layers[li]
-        p, s = dev_sets[r][li]
-        yy = y if y is not None else y_gate
-        return lambda: kl.check(lib.kf_int4_gemv(xs[li].data_ptr(), p.data_ptr(), s.data_ptr(), yy.data_ptr(),
-                                                 1, n, k, GROUP, stream_ptr), "gemv")
-
-    launches = [gemv_launch(i % copies) for i in range(8 * copies)]
-    for f in launches[:copies]:
-        f()
-    durs = timer.per_launch_ms(launches)
-    gate_avg_ms = statistics.fmean(durs)
-    gate_bytes = algo_bytes(1, gn, gk)
-    achieved = gate_bytes / (gate_avg_ms * 1e-3) / 1e9
-    log(f"gate GEMV avg {gate_avg_ms * 1e3:.2f} us over {len(durs)} launches -> {achieved:.0f} GB/s")
-
-    # --- per-layer isolated kernel times (reference protocol: median of per-launch events) ---------
+    # --- the other step structures ----------------------------------------------------------------
+    structures = {}
+    for label, fn, launches in (("decoder_4_launches", step_decoder, 4), ("separate_7_launches", step_separate, 7)):
+        gs = GraphSteps(torch, fn, copies)
+        ms = gs.event_avg_ms(8 * copies)
+        structures[label] = {"launches": launches, "us_per_step": round(ms * 1e3, 3),
+                             "gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                             "pct_of_copy": round(100 * step_bytes / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
+        log(f"{label}: {ms * 1e3:.2f} us/step")
     per_layer = {}
-    sum_med = 0.0
-    for li, (name, n, k, *_r) in enumerate(layers):
-        yl = torch.empty(1, n, dtype=torch.float16, device="cuda")
-        fl = [gemv_launch(i % copies, li, yl) for i in range(4 * copies)]
-        d = sorted(timer.per_launch_ms(fl))
-        med = statistics.median(d)
-        sum_med += med
-        b = algo_bytes(1, n, k)
-        per_layer[name] = {"N": n, "K": k, "bytes": b, "median_us": round(med * 1e3, 3),
-                           "p10_us": round(d[len(d) // 10] * 1e3, 3), "p90_us": round(d[(9 * len(d)) // 10] * 1e3, 3),
-                           "gbps": round(b / (med * 1e-3) / 1e9, 1),
-                           "pct_of_copy": round(100 * b / (med * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
-    isolated_gbps = step_bytes / (sum_med * 1e-3) / 1e9
+    for nm in names:
+        i = idx[nm]
+        gs = GraphSteps(torch, lambda r, nm=nm: single(r, nm), copies)
+        ms = gs.event_avg_ms(8 * copies)
+        b = algo_bytes(1, layers[i]["N"], layers[i]["K"])
+        per_layer[nm] = {"N": layers[i]["N"], "K": layers[i]["K"], "bytes": b, "us": round(ms * 1e3, 3),
+                         "gbps": round(b / (ms * 1e-3) / 1e9, 1),
+                         "pct_of_copy": round(100 * b / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
 
-    # --- M=2048: MFMA GEMM on every shape ------------------------------------------------------------
+    # --- M=2048: MFMA GEMM on every shape ------------------------------------------------------
     m2048 = None
     if not args.no_m2048:
         log("M=2048 GEMM leg")
-        mfma_peak = measure_mfma_peak(torch, timer)
+        mfma_peak = measure_mfma_peak(torch)
         total_flops, total_ms, per = 0.0, 0.0, {}
-        for li, (name, n, k, *_r) in enumerate(layers):
-            xm = torch.randn(2048, k, dtype=torch.float16, device="cuda")
-            p, s = dev_sets[0][li]
+        for i, ly in enumerate(layers):
+            xm = torch.randn(2048, ly["K"], dtype=torch.float16, device="cuda")
+            p, s = dev[0][i]
             ops.int4_gemm(xm, p, s, GROUP)
-            t = statistics.median(timer.batch_avg_ms(lambda: ops.int4_gemm(xm, p, s, GROUP), 5) for _ in range(5))
-            fl = 2.0 * 2048 * n * k
-            per[name] = {"us": round(t * 1e3, 1), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
+            t = statistics.median(batch_avg_ms(torch, lambda: ops.int4_gemm(xm, p, s, GROUP), 5) for _ in range(5))
+            fl = 2.0 * 2048 * ly["N"] * ly["K"]
+            per[ly["name"]] = {"us": round(t * 1e3, 1), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
             total_flops += fl
             total_ms += t
             del xm
@@ -317,7 +358,7 @@ def main() -> int:
                  "gate_frac_of_spec_peak": round(gate_tf / SPEC_FP16_TFLOPS, 4), "per_layer": per}
         log(f"M=2048 gate {gate_tf} TFLOPS; hipBLASLt fp16 peak {mfma_peak:.0f} TFLOPS")
 
-    # --- CPU baseline: the oracle's FP32 dequant + matmul on the host cores ------------------------
+    # --- CPU baseline: the oracle's FP32 dequant + matmul on the host cores --------------------
     cpu = None
     if not args.no_cpu:
         from threadpoolctl import threadpool_limits
@@ -325,7 +366,7 @@ def main() -> int:
         from oracle import int4_oracle as o
 
         threads = min(len(os.sched_getaffinity(0)), 16)
-        host = [(p.numpy(), s.numpy(), x.numpy()) for *_, p, s, x in layers]
+        host = [(ly["packed"].numpy(), ly["scales"].numpy(), ly["x"].numpy()) for ly in layers]
         with threadpool_limits(limits=threads):
             for p, s, x in host:  # warm-up
                 o.linear_ref_fp32(x, p, s, GROUP)
@@ -339,7 +380,8 @@ def main() -> int:
         med = statistics.median(times)
         cpu = {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": f"{len(times)} steps of the 7 TinyLlama linears at M=1 (oracle FP32 dequant+matmul, "
-                         f"numpy; BLAS on {threads} threads, unpack single-threaded); median {med * 1e3:.1f} ms/step",
+                         f"numpy; BLAS on {threads} threads, nibble unpack single-threaded); "
+                         f"median {med * 1e3:.1f} ms/step",
                "cpu_model": _cpu_model()}
         log(f"CPU baseline {cpu['value']} GB/s ({med * 1e3:.1f} ms/step)")
 
@@ -349,34 +391,26 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "tinyllama_7_linears_m1_g128", "shapes_NxK": [[n, k] for _, n, k in TL_LAYERS],
                    "group_size": GROUP, "bytes_per_step": step_bytes, "weight_copies_rotated": copies,
+                   "step": "one int4_linear_grouped launch over the 7 independent linears",
                    "graph_captured": True},
         "pct_of_measured_copy": round(100 * value / ceil["hbm_copy_gbps"], 1),
         "pct_of_measured_read": round(100 * value / ceil["hbm_read_gbps"], 1),
         "reference_pct_of_copy_on_its_gpu": REFERENCE_PCT_OF_COPY,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": SPEC_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / SPEC_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "gemv_kernel M=1 gate 5632x2048", "bytes_per_launch": gate_bytes,
-                     "avg_launch_us": round(gate_avg_ms * 1e3, 3),
-                     "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4)},
+                     "kernel": "kf::gemv_kernel<1,2,1> (grouped, 7 TinyLlama linears)",
+                     "bytes_per_launch": step_bytes, "avg_launch_us": round(gemv_avg_ms * 1e3, 3),
+                     "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4),
+                     "frac_of_measured_read": round(achieved / ceil["hbm_read_gbps"], 4)},
         "cpu_baseline": cpu,
         "ceilings": {k: round(v, 1) if isinstance(v, float) else v for k, v in ceil.items()},
-        "isolated_sum_of_medians_gbps": round(isolated_gbps, 1),
+        "step_structures": structures,
         "per_layer_m1": per_layer,
         "m2048": m2048,
         "device": props.name, "cu_count": props.multi_processor_count,
     }
     print(json.dumps(line), flush=True)
     return 0
-
-
-def _cpu_model() -> str:
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 if __name__ == "__main__":

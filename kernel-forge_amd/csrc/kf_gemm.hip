@@ -24,12 +24,13 @@ namespace {
 
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row (144 B, 16 B aligned)
+constexpr int kXcds = 8;
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool XCD_ORDER>
 __global__ __launch_bounds__(256) void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
                                                    const half_t* __restrict__ scales, half_t* __restrict__ y,
                                                    float* __restrict__ ws, int M, int N, int K, int log2_group,
-                                                   int kt_per_split) {
+                                                   int kt_per_split, int tiles_n, int tiles_total) {
   static_assert(WM * WN == 4, "256 threads = 4 wavefronts");
   constexpr int TM = BM / WM / 16;
   constexpr int TN = BN / WN / 16;
@@ -47,10 +48,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half_t* __restrict__ x,
   const int wave = tid >> 6;
   const int wm = wave / WN;
   const int wn = wave % WN;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
+  // Tile of this workgroup.  Consecutive workgroup ids rotate over the 8 XCDs;
+  // with XCD_ORDER each XCD takes a contiguous run of tiles (M-major), so the
+  // x rows and weight columns it touches stay in that XCD's L2.
+  const int bid = blockIdx.x;
+  int tile = bid;
+  if (XCD_ORDER) {
+    const int per_xcd = (tiles_total + kXcds - 1) / kXcds;
+    tile = (bid % kXcds) * per_xcd + bid / kXcds;
+  }
+  if (tile >= tiles_total) return;
+  const int tm = tile / tiles_n;
+  const int n0 = (tile - tm * tiles_n) * BN;
+  const int m0 = tm * BM;
   const int nkt = K / BK;
-  const int kt_begin = blockIdx.z * kt_per_split;
+  const int kt_begin = blockIdx.y * kt_per_split;
   const int kt_end = min(nkt, kt_begin + kt_per_split);
   const int words_per_row = K >> 3;
   const int groups_per_row = K >> log2_group;
@@ -145,7 +157,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half_t* __restrict__ x,
   // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
   const int out_col = lane & 15;
   const int out_row = (lane >> 4) * 4;
-  float* part = ws ? ws + (size_t)blockIdx.z * M * N : nullptr;
+  float* part = ws ? ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -176,27 +188,36 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
 
 struct TileCfg {
   int bm, bn;
+  bool xcd;
 };
-constexpr TileCfg kTiles[] = {{16, 128}, {32, 128}, {64, 128}, {128, 128}};
+// Tile table: index = GemmPlan::tile.
+constexpr TileCfg kTiles[] = {{16, 128, false}, {32, 128, false}, {64, 128, false}, {128, 128, false},
+                              {128, 128, true}, {64, 128, true}};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-typedef void (*GemmFn)(const half_t*, const uint32_t*, const half_t*, half_t*, float*, int, int, int, int, int);
+typedef void (*GemmFn)(const half_t*, const uint32_t*, const half_t*, half_t*, float*, int, int, int, int, int, int,
+                       int);
 
 GemmFn gemm_fn(int tile) {
   switch (tile) {
-    case 0: return gemm_kernel<16, 128, 1, 4>;
-    case 1: return gemm_kernel<32, 128, 1, 4>;
-    case 2: return gemm_kernel<64, 128, 2, 2>;
-    default: return gemm_kernel<128, 128, 2, 2>;
+    case 0: return gemm_kernel<16, 128, 1, 4, false>;
+    case 1: return gemm_kernel<32, 128, 1, 4, false>;
+    case 2: return gemm_kernel<64, 128, 2, 2, false>;
+    case 3: return gemm_kernel<128, 128, 2, 2, false>;
+    case 4: return gemm_kernel<128, 128, 2, 2, true>;
+    default: return gemm_kernel<64, 128, 2, 2, true>;
   }
 }
 
 }  // namespace
 
-GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
+int gemm_num_tiles() { return kNumTiles; }
+
+GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
   GemmPlan p;
-  p.tile = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
-  p.block_m = kTiles[p.tile].bm;
-  p.block_n = kTiles[p.tile].bn;
+  p.tile = tile;
+  p.block_m = kTiles[tile].bm;
+  p.block_n = kTiles[tile].bn;
   const int nkt = K / BK;
   const long tiles = (long)ceil_div(N, p.block_n) * ceil_div(M, p.block_m);
   const long want = 2L * (cu_count > 0 ? cu_count : 256);
@@ -212,6 +233,11 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
   return p;
 }
 
+GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
+  const int tile = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
+  return gemm_plan_with_tile(M, N, K, cu_count, tile);
+}
+
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
@@ -219,11 +245,13 @@ size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
                        void* ws, int M, int N, int K, int group_size, hipStream_t stream) {
   const int log2_group = group_size == 128 ? 7 : 6;
-  dim3 grid(ceil_div(N, p.block_n), ceil_div(M, p.block_m), p.splits);
+  const int tiles_n = ceil_div(N, p.block_n);
+  const int tiles_total = tiles_n * ceil_div(M, p.block_m);
+  const int grid_x = kTiles[p.tile].xcd ? ceil_div(tiles_total, kXcds) * kXcds : tiles_total;
   float* part = p.splits > 1 ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(gemm_fn(p.tile), grid, dim3(256), 0, stream, static_cast<const half_t*>(x),
+  hipLaunchKernelGGL(gemm_fn(p.tile), dim3(grid_x, p.splits), dim3(256), 0, stream, static_cast<const half_t*>(x),
                      static_cast<const uint32_t*>(packed), static_cast<const half_t*>(scales),
-                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split);
+                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split, tiles_n, tiles_total);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const size_t mn = (size_t)M * N;

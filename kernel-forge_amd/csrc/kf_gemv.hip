@@ -262,20 +262,25 @@ GemvFn pick(int M, int R, int U) {
 
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   GemvPlan p;
+  const long cus = cu_count > 0 ? cu_count : 256;
   long rows = 0;
   int max_chunks = 0;
   for (int i = 0; i < count; ++i) {
     rows += N[i];
     if (K[i] / 32 > max_chunks) max_chunks = K[i] / 32;
   }
-  // Largest pass (in 64-chunk blocks) a wave may issue at once; register
-  // pressure grows with M, so fewer blocks per pass for larger M.
+  // Two rows per wave once that still leaves >= 8 wavefronts per CU
+  // (measured on MI355X: q/o 2048x2048 alone prefers one row, gate 5632x2048
+  // and every grouped decode set prefer two; four is always slower).
+  p.rows_per_wave = (rows + 1) / 2 >= 8 * cus ? 2 : 1;
+  const long waves = (rows + p.rows_per_wave - 1) / p.rows_per_wave;
+  // Deep passes (several 64-chunk blocks per round trip) pay off only when
+  // the launch has few wavefronts: down 2048x5632 alone is fastest with 3
+  // blocks per pass, the 7-layer group with 1 (the registers of a deep pass
+  // cost more occupancy than the extra memory parallelism returns).
   const int blocks = ceil_div(max_chunks, 64);
   const int u_max = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
-  p.unroll = blocks < u_max ? blocks : u_max;
-  // Two rows per wave once that still leaves >= 8 wavefronts per CU.
-  const long target_waves = 8L * (cu_count > 0 ? cu_count : 256);
-  p.rows_per_wave = (rows + 1) / 2 >= target_waves ? 2 : 1;
+  p.unroll = waves >= 12 * cus ? 1 : (blocks < u_max ? blocks : u_max);
   return p;
 }
 

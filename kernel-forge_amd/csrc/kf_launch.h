@@ -54,6 +54,9 @@ struct GemmPlan {
   int kt_per_split;// k-tiles of 64 per split
 };
 GemmPlan gemm_plan(int M, int N, int K, int cu_count);
+// Plan with an explicit tile-table entry (used by the measured dispatcher table and tuning).
+GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile);
+int gemm_num_tiles();
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N);
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
                        void* ws, int M, int N, int K, int group_size, hipStream_t stream);
