@@ -43,10 +43,14 @@ Protocol
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -80,7 +84,48 @@ def parse_args():
     ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "copy"],
                     help="only launch one kernel --profile-iters times (for rocprofv3 --pmc runs) and exit")
     ap.add_argument("--profile-iters", type=int, default=20)
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     return ap.parse_args()
+
+
+def _pmc_median_kib(counter: str, profile: str, kernel_substr: str, outdir: str) -> float | None:
+    """Runs this script under `rocprofv3 --pmc <counter>` in --profile mode; median KiB per dispatch."""
+    name = f"{profile}_{counter}"
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", name, "--",
+           sys.executable, "-u", str(Path(__file__).resolve()), "--profile", profile, "--profile-iters", "10"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        subprocess.run(cmd, timeout=120, capture_output=True, env=env, cwd="/tmp")
+    except (OSError, subprocess.SubprocessError):
+        return None
+    vals = []
+    for f in Path(outdir).rglob(f"{name}*counter_collection.csv"):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                if kernel_substr in row.get("Kernel_Name", "") and row.get("Counter_Name") == counter:
+                    vals.append(float(row["Counter_Value"]))
+    return statistics.median(vals) if vals else None
+
+
+def measure_traffic() -> dict | None:
+    """HBM bytes per grouped-GEMV launch from FETCH_SIZE and WRITE_SIZE, each calibrated against a
+    64 MiB copy (known to read and write 65,536 KiB).  Runs before this process touches the GPU;
+    returns None when rocprofv3 is unavailable or a pass fails."""
+    if shutil.which("rocprofv3") is None:
+        return None
+    outdir = tempfile.mkdtemp(prefix="kf_pmc_")
+    try:
+        cf = _pmc_median_kib("FETCH_SIZE", "copy", "bw_copy_kernel", outdir)
+        cw = _pmc_median_kib("WRITE_SIZE", "copy", "bw_copy_kernel", outdir)
+        gf = _pmc_median_kib("FETCH_SIZE", "gemv_grouped", "gemv_kernel", outdir)
+        gw = _pmc_median_kib("WRITE_SIZE", "gemv_grouped", "gemv_kernel", outdir)
+    finally:
+        shutil.rmtree(outdir, ignore_errors=True)
+    if not all(v for v in (cf, cw, gf)) or gw is None:
+        return None
+    fetch_factor, write_factor = 65536.0 / cf, 65536.0 / cw
+    return {"bytes": (gf * fetch_factor + gw * write_factor) * 1024.0, "fetch_kib": gf, "write_kib": gw,
+            "fetch_factor": round(fetch_factor, 4), "write_factor": round(write_factor, 4)}
 
 
 def profile_only(args, torch, lib, kl, ops, kq) -> int:
@@ -247,6 +292,12 @@ def main() -> int:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
               "This build has no multi-GPU path; run with --gpus 1.", file=sys.stderr)
         return 2
+    traffic = None
+    if not args.profile and not args.no_traffic:
+        log("rocprofv3 FETCH_SIZE / WRITE_SIZE passes (child processes)")
+        traffic = measure_traffic()
+        log(f"traffic: {traffic}")
+
     import torch
 
     from kernelforge import _lib as kl
@@ -397,7 +448,9 @@ def main() -> int:
         "pct_of_measured_read": round(100 * value / ceil["hbm_read_gbps"], 1),
         "reference_pct_of_copy_on_its_gpu": REFERENCE_PCT_OF_COPY,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": SPEC_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / SPEC_HBM_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / SPEC_HBM_GBPS, 4),
+                     "traffic": round(traffic["bytes"]) if traffic else None,
+                     "traffic_detail": traffic,
                      "kernel": "kf::gemv_kernel<1,2,1> (grouped, 7 TinyLlama linears)",
                      "bytes_per_launch": step_bytes, "avg_launch_us": round(gemv_avg_ms * 1e3, 3),
                      "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4),
