@@ -215,6 +215,8 @@ int gemm_num_tiles() { return kNumTiles; }
 
 GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
   GemmPlan p;
+  p.skinny = false;
+  p.sk = SkinnyPlan{0, 0, 0};
   p.tile = tile;
   p.block_m = kTiles[tile].bm;
   p.block_n = kTiles[tile].bn;
@@ -234,16 +236,24 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
 }
 
 GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
+  if (M <= kSkinnyMaxM && K % 128 == 0) {
+    GemmPlan p = gemm_plan_with_tile(M, N, K, cu_count, 0);
+    p.skinny = true;
+    p.splits = 1;
+    p.sk = skinny_plan(M, N, K, cu_count);
+    return p;
+  }
   const int tile = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
   return gemm_plan_with_tile(M, N, K, cu_count, tile);
 }
 
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
-  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  return !p.skinny && p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
                        void* ws, int M, int N, int K, int group_size, hipStream_t stream) {
+  if (p.skinny) return skinny_launch(p.sk, x, packed, scales, y, M, N, K, group_size, stream);
   const int log2_group = group_size == 128 ? 7 : 6;
   const int tiles_n = ceil_div(N, p.block_n);
   const int tiles_total = tiles_n * ceil_div(M, p.block_m);

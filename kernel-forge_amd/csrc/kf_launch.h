@@ -45,8 +45,23 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
                        hipStream_t stream);
 
+// ---- skinny MFMA GEMM (M <= 64, K % 128 == 0): one weight stream, K split in-block ----
+// Measured on MI355X (dispatch_sweep.py): at M=64 the tiled GEMM is faster on 4 of 6 shapes,
+// at M=32 the skinny kernel wins on 5 of 6.
+constexpr int kSkinnyMaxM = 32;
+struct SkinnyPlan {
+  int m_tiles;   // 16-row tiles of M (1..4)
+  int ks_waves;  // wavefronts per workgroup, each a contiguous run of 128-k super-steps
+  int unroll;    // super-steps whose weight loads are in flight together
+};
+SkinnyPlan skinny_plan(int M, int N, int K, int cu_count);
+hipError_t skinny_launch(const SkinnyPlan& p, const void* x, const void* packed, const void* scales, void* y, int M,
+                         int N, int K, int group_size, hipStream_t stream);
+
 // ---- MFMA GEMM (any M, N % 64 == 0) --------------------------------------
 struct GemmPlan {
+  bool skinny;     // true: the skinny kernel (fields below unused except sk)
+  SkinnyPlan sk;
   int tile;        // index into the tile table (kf_gemm.hip)
   int block_m;     // BM
   int block_n;     // BN

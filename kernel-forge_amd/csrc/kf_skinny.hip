@@ -1,0 +1,147 @@
+// "Skinny" INT4 GEMM for small M (M <= 64) on gfx950: a weight stream with matrix-core math.
+//
+// y[M, N] = x[M, K] @ W_hat^T with W_hat = fp16_rne(q * s) (the same operand the tiled GEMM
+// and the reference's tensor-core kernel use, dequant_gemm_tc_kernel.cuh:100-112), fp32
+// accumulation, fp16 RNE output.
+//
+// At small M the weights are the traffic: the tiled GEMM re-stages them through LDS per
+// M-tile and splits K through a global workspace, and the GEMV spends 4 dot2 per 8 weights
+// per row of x.  Here every weight is read from HBM exactly once and dequantized once, and
+// all rows of x share it through v_mfma_f32_16x16x32_f16:
+//   * A workgroup owns 16 output columns (weight rows n0..n0+15) and splits K over its KS
+//     wavefronts; wavefront w takes a contiguous run of 128-k "super-steps".
+//   * Lane l serves column n0 + l%16 and k-quarter g = l/16 of each super-step: one dwordx4
+//     of packed words per lane covers k = 128s + 32g .. +31 of its column, so a wavefront
+//     instruction streams 16 columns x 128 k = 1 KiB.
+//   * MFMA sub-step t (0..3) of super-step s gives lane l the k range 128s + 32g + 8t .. +7
+//     for both operands: B = dequant8(word t) of its column, A = 8 consecutive x values of
+//     row (16*mt + l%16).  Since A and B agree on which k each (lane group, slot) holds, the
+//     MFMA sums exactly the 128 k of the super-step.
+//   * Weight loads of UU super-steps are issued before their math (one round trip per pass);
+//     x comes from L2.
+//   * The KS partial 16 x 16*MT tiles are summed in fixed wavefront order through LDS
+//     (deterministic) and written as fp16.  Rows past M read row M-1 and are never stored;
+//     columns past N read row N-1 and are never stored.
+#include "kf_device.h"
+#include "kf_launch.h"
+
+namespace kf {
+namespace {
+
+template <int MT, int U>
+__global__ __launch_bounds__(1024) void skinny_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
+                                                      const half_t* __restrict__ scales, half_t* __restrict__ y,
+                                                      int M, int N, int K, int log2_group) {
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][MT * 256]
+  const int ks_waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int n = min(n0 + col, N - 1);
+  const int nss = K >> 7;  // 128-k super-steps
+  const int ss_begin = (wave * nss) / ks_waves;
+  const int ss_end = ((wave + 1) * nss) / ks_waves;
+
+  const uint32_t* wrow = packed + (size_t)n * (K >> 3) + 4 * g;
+  const half_t* srow = scales + (size_t)n * (K >> log2_group);
+  const half_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = x + (size_t)min(16 * mt + col, M - 1) * K + 32 * g;
+
+  float4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int ss = ss_begin; ss < ss_end; ss += U) {
+    u32x4 wv[U];
+    half_t sv[U];
+    half8_t xa[U][MT][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = min(ss + u, ss_end - 1);  // in range; repeats are masked below
+      wv[u] = load_u32x4_stream(wrow + 16 * s);
+      sv[u] = srow[(128 * s + 32 * g) >> log2_group];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xa[u][mt][t] = *reinterpret_cast<const half8_t*>(xrow[mt] + 128 * s + 8 * t);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (ss + u < ss_end) {  // uniform
+        const half2_t s2 = {sv[u], sv[u]};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const half8_t b = dequant8(wv[u][t], s2);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u][mt][t], b, acc[mt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // Fixed-order reduction of the KS partial tiles.  MFMA result layout: lane l,
+  // element r holds row 4*(l/16)+r of the 16-row tile, column l%16.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    *reinterpret_cast<float4_t*>(&red[wave * (MT * 256) + mt * 256 + 4 * lane]) = acc[mt];
+  __syncthreads();
+  for (int i = threadIdx.x; i < MT * 256; i += blockDim.x) {
+    float sum = 0.0f;
+    for (int w = 0; w < ks_waves; ++w) sum += red[w * (MT * 256) + i];
+    const int mt = i >> 8, l = (i >> 2) & 63, r = i & 3;
+    const int row = 16 * mt + 4 * (l >> 4) + r;
+    const int c = n0 + (l & 15);
+    if (row < M && c < N) y[(size_t)row * N + c] = (half_t)sum;
+  }
+}
+
+typedef void (*SkinnyFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int, int);
+
+SkinnyFn skinny_fn(int mt, int u) {
+  switch (mt) {
+    case 1: return u >= 4 ? skinny_kernel<1, 4> : (u == 2 ? skinny_kernel<1, 2> : skinny_kernel<1, 1>);
+    case 2: return u >= 2 ? skinny_kernel<2, 2> : skinny_kernel<2, 1>;
+    case 3: return skinny_kernel<3, 1>;
+    default: return skinny_kernel<4, 1>;
+  }
+}
+
+}  // namespace
+
+SkinnyPlan skinny_plan(int M, int N, int K, int cu_count) {
+  SkinnyPlan p;
+  p.m_tiles = ceil_div(M, 16);
+  const int groups = ceil_div(N, 16);
+  const int nss = K / 128;
+  const long target = 8L * (cu_count > 0 ? cu_count : 256);  // wavefronts to keep HBM busy
+  int ks = 4;
+  while (ks < 16 && (long)groups * ks < target && nss / (ks * 2) >= 1) ks *= 2;
+  if (ks > nss) ks = nss > 0 ? nss : 1;
+  while (ks > 4 && ks * p.m_tiles > 8) ks /= 2;  // reduction buffer <= 32 KiB of LDS
+  p.ks_waves = ks;
+  // Super-steps whose weight loads are in flight together; x fragments cost 16 VGPRs per
+  // 16-row tile per super-step, so fewer for more rows.
+  const int per_wave = ceil_div(nss, ks);
+  const int u_max = p.m_tiles == 1 ? 4 : (p.m_tiles == 2 ? 2 : 1);
+  int u = per_wave < u_max ? per_wave : u_max;
+  if (u == 3) u = 2;
+  p.unroll = u < 1 ? 1 : u;
+  return p;
+}
+
+hipError_t skinny_launch(const SkinnyPlan& p, const void* x, const void* packed, const void* scales, void* y, int M,
+                         int N, int K, int group_size, hipStream_t stream) {
+  const int log2_group = group_size == 128 ? 7 : 6;
+  const size_t lds = (size_t)p.ks_waves * p.m_tiles * 256 * sizeof(float);
+  hipLaunchKernelGGL(skinny_fn(p.m_tiles, p.unroll), dim3(ceil_div(N, 16)), dim3(64 * p.ks_waves), lds, stream,
+                     static_cast<const half_t*>(x), static_cast<const uint32_t*>(packed),
+                     static_cast<const half_t*>(scales), static_cast<half_t*>(y), M, N, K, log2_group);
+  return hipGetLastError();
+}
+
+}  // namespace kf

@@ -17,10 +17,11 @@ import torch
 
 from kernelforge import _lib
 
-# Measured GEMV/GEMM crossover on one MI355X: the largest M at which the sum of
-# GEMV times over the layer shapes beats the GEMM's (reference rule,
-# bench/sweep_int4_dispatch.py:51-57).
-GEMV_MAX_M = 8
+# Measured GEMV/GEMM crossover on one MI355X (kernelforge/dispatch_sweep.py): the
+# largest M at which the sum of GEMV times over the layer shapes beats the GEMM's
+# (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
+# skinny MFMA kernel (M <= 32), then the tiled MFMA GEMM.
+GEMV_MAX_M = 3
 
 
 def _stream_ptr(device: torch.device) -> int:

@@ -220,13 +220,16 @@ def test_gemm_rejects_n_not_multiple_of_64():
         ops.int4_gemm(x, dp, ds, 128)
 
 
-def test_splitk_is_deterministic():
-    """Split-K partials are reduced in fixed order: repeated calls are bitwise identical."""
-    n, k = LAYER_SHAPES["tinyllama_gate_up"]
+@pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, True), ("tinyllama_gate_up", 16, False),
+                                             ("tinyllama_down", 64, False)])
+def test_gemm_is_deterministic(layer, m, splitk):
+    """Split-K partials (tiled GEMM) and the skinny kernel's per-wave K slices are reduced in
+    fixed order: repeated calls are bitwise identical."""
+    n, k = LAYER_SHAPES[layer]
     _, _, dp, ds = _weights(n, k, 128)
-    x = torch.from_numpy(_x(16, k, 99)).to(DEV)
-    ws = _lib.load().kf_int4_gemm_workspace_bytes(16, n, k, 128)
-    assert ws > 0, "expected a split-K plan at M=16"
+    x = torch.from_numpy(_x(m, k, 99)).to(DEV)
+    ws = _lib.load().kf_int4_gemm_workspace_bytes(m, n, k, 128)
+    assert (ws > 0) == splitk, f"expected {'a' if splitk else 'no'} split-K workspace at M={m}"
     outs = [ops.int4_gemm(x, dp, ds, 128) for _ in range(3)]
     assert all(torch.equal(outs[0], o_) for o_ in outs[1:])
 
