@@ -85,6 +85,7 @@ def parse_args():
                     help="only launch one kernel --profile-iters times (for rocprofv3 --pmc runs) and exit")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the TinyLlama graph-decode leg (config 5)")
     return ap.parse_args()
 
 
@@ -163,6 +164,47 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
     torch.cuda.synchronize()
     print(f"profiled {args.profile} x{args.profile_iters}", flush=True)
     return 0
+
+
+def e2e_decode(torch, prompt_len: int = 16, new_tokens: int = 128) -> dict:
+    """random-init TinyLlama architecture, greedy decode with one HIP-graph-captured
+    step, tokens/s over `new_tokens` back-to-back replays.  INT4 (q|k|v and gate|up fused), INT4
+    with the 7 linears unfused, and the same network with fp16 nn.Linear layers (hipBLASLt)."""
+    import dataclasses
+
+    from kernelforge import tinyllama as tl
+
+    dev = torch.device("cuda")
+    cfg = dataclasses.replace(tl.TinyLlamaConfig(), max_seq=prompt_len + new_tokens + 1)
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=torch.Generator().manual_seed(7)).to(dev)
+    out = {"model": "tinyllama-1.1b-arch random-init", "layers": cfg.layers, "prompt": prompt_len,
+           "new_tokens": new_tokens}
+
+    def run(model):
+        dec = tl.GraphDecoder(model, dev)
+        dec.prefill(prompt)
+        dec.capture()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.decode(new_tokens)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        return new_tokens / dt, dec.generated(prompt_len, new_tokens)
+
+    for label, kw in (("int4_fused", {"fuse": True}), ("int4_unfused", {"fuse": False})):
+        model = tl.build_int4_model(cfg, dev, seed=0, **kw)
+        tps, toks = run(model)
+        out[f"{label}_tok_s"] = round(tps, 1)
+        out[f"{label}_first_tokens"] = toks[:8].tolist()
+        del model
+        torch.cuda.empty_cache()
+    with torch.device(dev):
+        fp16 = tl.TinyLlama(cfg)
+    fp16.init_random_(0).half().eval()
+    out["fp16_tok_s"] = round(run(fp16)[0], 1)
+    del fp16
+    torch.cuda.empty_cache()
+    return out
 
 
 def log(msg: str) -> None:
@@ -409,6 +451,14 @@ def main() -> int:
                  "gate_frac_of_spec_peak": round(gate_tf / SPEC_FP16_TFLOPS, 4), "per_layer": per}
         log(f"M=2048 gate {gate_tf} TFLOPS; hipBLASLt fp16 peak {mfma_peak:.0f} TFLOPS")
 
+    # --- config 5: end-to-end graph decode ------------------------------------------------------
+    e2e = None
+    if not args.no_e2e:
+        log("TinyLlama graph decode leg")
+        e2e = e2e_decode(torch)
+        log(f"decode tok/s: int4 fused {e2e['int4_fused_tok_s']}, unfused {e2e['int4_unfused_tok_s']}, "
+            f"fp16 {e2e['fp16_tok_s']}")
+
     # --- CPU baseline: the oracle's FP32 dequant + matmul on the host cores --------------------
     cpu = None
     if not args.no_cpu:
@@ -460,6 +510,7 @@ def main() -> int:
         "step_structures": structures,
         "per_layer_m1": per_layer,
         "m2048": m2048,
+        "e2e_decode": e2e,
         "device": props.name, "cu_count": props.multi_processor_count,
     }
     print(json.dumps(line), flush=True)

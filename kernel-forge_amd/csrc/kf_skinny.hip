@@ -114,15 +114,19 @@ SkinnyFn skinny_fn(int mt, int u) {
 }  // namespace
 
 SkinnyPlan skinny_plan(int M, int N, int K, int cu_count) {
+  (void)N;
+  (void)cu_count;
   SkinnyPlan p;
   p.m_tiles = ceil_div(M, 16);
-  const int groups = ceil_div(N, 16);
+  // The K split depends on K (and M) only, never on N: a column's result is then the same
+  // whatever other rows share the launch, so concatenating q|k|v or gate|up rows is
+  // bit-identical to separate calls.  At least two 128-k super-steps per wavefront, at
+  // most 16 wavefronts, and a reduction buffer of at most 32 KiB of LDS.
   const int nss = K / 128;
-  const long target = 8L * (cu_count > 0 ? cu_count : 256);  // wavefronts to keep HBM busy
-  int ks = 4;
-  while (ks < 16 && (long)groups * ks < target && nss / (ks * 2) >= 1) ks *= 2;
-  if (ks > nss) ks = nss > 0 ? nss : 1;
-  while (ks > 4 && ks * p.m_tiles > 8) ks /= 2;  // reduction buffer <= 32 KiB of LDS
+  int ks = nss / 2;
+  if (ks > 16) ks = 16;
+  if (ks < 1) ks = 1;
+  while (ks * p.m_tiles > 32) --ks;
   p.ks_waves = ks;
   // Super-steps whose weight loads are in flight together; x fragments cost 16 VGPRs per
   // 16-row tile per super-step, so fewer for more rows.

@@ -1,0 +1,302 @@
+"""A TinyLlama-architecture decoder whose linears run on the INT4 path.
+
+Random-initialized (no checkpoints are fetched): 22 layers, hidden 2048, 32 query / 4 KV heads
+of dim 64, SwiGLU intermediate 5632, RMSNorm, RoPE, vocab 32000, fp16 activations.  The seven
+decoder linears of every layer are ``nn.Linear`` modules named like Hugging Face's
+(q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj), so ``quantize_linears_`` swaps
+them for ``KFLinearInt4`` exactly as it would in an HF model (reference
+kernelforge/modules.py:51-65); embedding and lm_head stay fp16.
+
+``fuse_decoder_linears_`` replaces q|k|v and gate|up by one INT4 module each whose packed rows are
+the concatenation of the originals (the packed format is per row, so this is the same format).
+For M <= 32 (decode and short prompts: the GEMV and skinny kernels, whose per-column arithmetic
+does not depend on N) the fused results are bit-identical; for larger M the tiled GEMM may pick a
+different split-K count for the wider matrix, which changes only the fp32 summation order.
+
+Decode follows the reference's graph method (bench/e2e_model.py:85-141): static KV cache,
+positions in device tensors, one decode step captured in a HIP graph and replayed; the greedy
+token is written back into the graph's input on the device, so replays run back to back.
+Attention is plain PyTorch (fp16 matmuls on contiguous operands, fp32 softmax).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from kernelforge import ops
+from kernelforge.modules import KFLinearInt4
+
+
+@dataclass
+class TinyLlamaConfig:
+    vocab: int = 32000
+    hidden: int = 2048
+    layers: int = 22
+    heads: int = 32
+    kv_heads: int = 4
+    head_dim: int = 64
+    intermediate: int = 5632
+    rms_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    max_seq: int = 160
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(x.dtype)
+
+
+def _rope_tables(cfg: TinyLlamaConfig, device) -> tuple[torch.Tensor, torch.Tensor]:
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
+    t = torch.arange(cfg.max_seq, dtype=torch.float32)
+    freqs = torch.outer(t, inv)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(device), emb.sin().to(device)
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+
+
+class FusedInt4Linear(nn.Module):
+    """Several INT4 linears on the same input as ONE GEMV/GEMM over their concatenated rows.
+
+    Bit-identical to running them separately for M <= 32 (GEMV and skinny kernels compute each
+    column independently of N); above that the tiled GEMM's split-K count may differ, which only
+    reorders fp32 sums.  Returns the per-part outputs.
+    """
+
+    def __init__(self, parts: list[KFLinearInt4]):
+        super().__init__()
+        g = {p.group_size for p in parts}
+        k = {p.in_features for p in parts}
+        if len(g) != 1 or len(k) != 1 or any(p.bias is not None for p in parts):
+            raise ValueError("fused parts need one group size, one in_features and no bias")
+        self.group_size = g.pop()
+        self.in_features = k.pop()
+        self.splits = [p.out_features for p in parts]
+        self.register_buffer("packed", torch.cat([p.packed for p in parts], dim=0).contiguous())
+        self.register_buffer("scales", torch.cat([p.scales for p in parts], dim=0).contiguous())
+
+    def forward(self, x: torch.Tensor) -> list[torch.Tensor]:
+        y = ops.int4_linear(x, self.packed, self.scales, self.group_size)
+        return list(torch.split(y, self.splits, dim=-1))
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: TinyLlamaConfig):
+        super().__init__()
+        self.cfg = cfg
+        h, d = cfg.hidden, cfg.head_dim
+        self.q_proj = nn.Linear(h, cfg.heads * d, bias=False)
+        self.k_proj = nn.Linear(h, cfg.kv_heads * d, bias=False)
+        self.v_proj = nn.Linear(h, cfg.kv_heads * d, bias=False)
+        self.o_proj = nn.Linear(cfg.heads * d, h, bias=False)
+        self.qkv: FusedInt4Linear | None = None
+
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
+        """x [1, T, H]; pos int64 [T] positions; cache_* [kv_heads, max_seq, d]; mask [T, max_seq]."""
+        cfg = self.cfg
+        t = x.shape[1]
+        if self.qkv is not None:
+            q, k, v = self.qkv(x)
+        else:
+            q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        q = q.view(t, cfg.heads, cfg.head_dim).transpose(0, 1)        # [Hq, T, d]
+        k = k.view(t, cfg.kv_heads, cfg.head_dim).transpose(0, 1)     # [Hkv, T, d]
+        v = v.view(t, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
+        c, s = cos[pos].to(q.dtype), sin[pos].to(q.dtype)              # [T, d]
+        q = q * c + _rotate_half(q) * s
+        k = k * c + _rotate_half(k) * s
+        cache_k.index_copy_(1, pos, k)
+        cache_v.index_copy_(1, pos, v)
+        rep = cfg.heads // cfg.kv_heads
+        kk = cache_k.repeat_interleave(rep, dim=0)                     # [Hq, S, d]
+        vv = cache_v.repeat_interleave(rep, dim=0)
+        scores = torch.bmm(q.contiguous(), kk.transpose(1, 2).contiguous()).float() / math.sqrt(cfg.head_dim)
+        scores = scores + mask                                         # [Hq, T, S]
+        probs = torch.softmax(scores, dim=-1).to(q.dtype)
+        out = torch.bmm(probs, vv.contiguous())                        # [Hq, T, d]
+        out = out.transpose(0, 1).reshape(1, t, cfg.heads * cfg.head_dim)
+        return self.o_proj(out)
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: TinyLlamaConfig):
+        super().__init__()
+        self.gate_proj = nn.Linear(cfg.hidden, cfg.intermediate, bias=False)
+        self.up_proj = nn.Linear(cfg.hidden, cfg.intermediate, bias=False)
+        self.down_proj = nn.Linear(cfg.intermediate, cfg.hidden, bias=False)
+        self.gate_up: FusedInt4Linear | None = None
+
+    def forward(self, x):
+        if self.gate_up is not None:
+            g, u = self.gate_up(x)
+        else:
+            g, u = self.gate_proj(x), self.up_proj(x)
+        return self.down_proj(torch.nn.functional.silu(g) * u)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: TinyLlamaConfig):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden, cfg.rms_eps)
+        self.self_attn = Attention(cfg)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden, cfg.rms_eps)
+        self.mlp = MLP(cfg)
+
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
+        x = x + self.self_attn(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, mask)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class TinyLlama(nn.Module):
+    def __init__(self, cfg: TinyLlamaConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.embed_tokens = nn.Embedding(cfg.vocab, cfg.hidden)
+        self.layers = nn.ModuleList(DecoderLayer(cfg) for _ in range(cfg.layers))
+        self.norm = RMSNorm(cfg.hidden, cfg.rms_eps)
+        self.lm_head = nn.Linear(cfg.hidden, cfg.vocab, bias=False)
+
+    @torch.no_grad()
+    def init_random_(self, seed: int = 0) -> "TinyLlama":
+        """Seeded N(0, 0.02^2) linear weights and N(0, 1) embeddings, drawn on the module's device."""
+        dev = self.embed_tokens.weight.device
+        g = torch.Generator(device=dev).manual_seed(seed)
+        for mod in self.modules():
+            if isinstance(mod, nn.Linear):
+                mod.weight.copy_(torch.randn(mod.weight.shape, generator=g, device=dev) * 0.02)
+            elif isinstance(mod, nn.Embedding):
+                mod.weight.copy_(torch.randn(mod.weight.shape, generator=g, device=dev))
+        return self
+
+
+    def new_cache(self, device, dtype=torch.float16) -> torch.Tensor:
+        c = self.cfg
+        return torch.zeros(c.layers, 2, c.kv_heads, c.max_seq, c.head_dim, device=device, dtype=dtype)
+
+    @torch.no_grad()
+    def forward(self, tokens, pos, cache, rope, mask):
+        """tokens int64 [T]; pos int64 [T]; returns logits of the last position, [vocab] fp32.
+        Inference only (no autograd)."""
+        cos, sin = rope
+        x = self.embed_tokens(tokens).unsqueeze(0)
+        for i, layer in enumerate(self.layers):
+            x = layer(x, pos, cos, sin, cache[i, 0], cache[i, 1], mask)
+        x = self.norm(x[:, -1:])
+        return self.lm_head(x).float().view(-1)
+
+
+def causal_mask(pos: torch.Tensor, max_seq: int) -> torch.Tensor:
+    """[T, max_seq] additive mask: 0 where key index <= query position, -inf elsewhere."""
+    keys = torch.arange(max_seq, device=pos.device)
+    return torch.where(keys[None, :] <= pos[:, None], 0.0, float("-inf")).float()
+
+
+@torch.no_grad()
+def fuse_decoder_linears_(model: TinyLlama) -> int:
+    """Fuses q|k|v and gate|up INT4 linears of every layer (after quantize_linears_)."""
+    n = 0
+    for layer in model.layers:
+        a, m = layer.self_attn, layer.mlp
+        if all(isinstance(p, KFLinearInt4) for p in (a.q_proj, a.k_proj, a.v_proj)):
+            a.qkv = FusedInt4Linear([a.q_proj, a.k_proj, a.v_proj])
+            n += 1
+        if all(isinstance(p, KFLinearInt4) for p in (m.gate_proj, m.up_proj)):
+            m.gate_up = FusedInt4Linear([m.gate_proj, m.up_proj])
+            n += 1
+    return n
+
+
+class GraphDecoder:
+    """Greedy decode with one HIP-graph-captured step (static cache, device-side positions).
+
+    The captured step reads the current token and position from static device tensors, runs
+    the model, writes argmax into the token buffer and the output history, and advances the
+    position, so replays need no host round trip.
+    """
+
+    def __init__(self, model: TinyLlama, device):
+        self.model, self.device = model, device
+        cfg = model.cfg
+        self.rope = _rope_tables(cfg, device)
+        self.cache = model.new_cache(device)
+        self.token = torch.zeros(1, dtype=torch.long, device=device)
+        self.pos = torch.zeros(1, dtype=torch.long, device=device)
+        self.history = torch.zeros(cfg.max_seq, dtype=torch.long, device=device)
+        self.graph = None
+
+    def _step(self):
+        mask = causal_mask(self.pos, self.model.cfg.max_seq)
+        logits = self.model(self.token, self.pos, self.cache, self.rope, mask)
+        nxt = torch.argmax(logits).view(1)
+        self.history.index_copy_(0, self.pos + 1, nxt)
+        self.token.copy_(nxt)
+        self.pos.add_(1)
+
+    def prefill(self, prompt: torch.Tensor) -> None:
+        """Runs the prompt eagerly; leaves the first generated token in self.token."""
+        t = prompt.numel()
+        pos = torch.arange(t, device=self.device)
+        self.cache.zero_()
+        logits = self.model(prompt, pos, self.cache, self.rope, causal_mask(pos, self.model.cfg.max_seq))
+        self.history.zero_()
+        self.history[:t] = prompt
+        self.token.copy_(torch.argmax(logits).view(1))
+        self.history[t] = self.token[0]
+        self.pos.fill_(t)
+
+    def capture(self) -> None:
+        saved = (self.cache.clone(), self.token.clone(), self.pos.clone(), self.history.clone())
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        # capture ran warm-up steps; restore the state after prefill
+        self.cache.copy_(saved[0])
+        self.token.copy_(saved[1])
+        self.pos.copy_(saved[2])
+        self.history.copy_(saved[3])
+
+    def decode(self, steps: int, use_graph: bool = True) -> torch.Tensor:
+        for _ in range(steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self._step()
+        return self.history
+
+    def generated(self, prompt_len: int, steps: int) -> torch.Tensor:
+        return self.history[prompt_len:prompt_len + steps + 1].clone()
+
+
+def build_int4_model(cfg: TinyLlamaConfig, device, seed: int = 0, group_size: int = 128,
+                     fuse: bool = True) -> TinyLlama:
+    """Random-init TinyLlama on `device` in fp16 with every decoder linear on the INT4 path."""
+    from kernelforge.modules import quantize_linears_
+
+    with torch.device(device):
+        model = TinyLlama(cfg)
+    model.init_random_(seed).half()
+    quantize_linears_(model, group_size)
+    if fuse:
+        fuse_decoder_linears_(model)
+    return model.eval()
