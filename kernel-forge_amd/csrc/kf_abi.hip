@@ -137,8 +137,11 @@ int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
   int cus = 0;
   if ((st = cu_count(&cus))) return st;
   const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);
-  if ((long)(M + plan.block_m - 1) / plan.block_m > 65535)
-    return fail(KF_ERR_UNSUPPORTED, "M=%d exceeds the grid limit for a %d-row tile", M, plan.block_m);
+  // One workgroup (<= 512 threads) per output tile, all in grid dimension x.
+  const long long tiles = (long long)((M + plan.block_m - 1) / plan.block_m) * ((N + plan.block_n - 1) / plan.block_n);
+  if (!plan.skinny && (tiles + 8) * 512 > 0x7FFFFFFFLL)
+    return fail(KF_ERR_UNSUPPORTED, "M=%d, N=%d exceed the grid limit for %dx%d tiles", M, N, plan.block_m,
+                plan.block_n);
   const size_t need = kf::gemm_workspace_bytes(plan, M, N);
   if (need > 0) {
     if (!ws) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got NULL", need);

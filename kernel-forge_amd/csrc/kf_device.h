@@ -55,6 +55,36 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
   return out;
 }
 
+// The same unpack with its two constants held in registers.  gfx9 VOP3 encodings take no
+// literal operand and at most one SGPR, so without this the compiler splits every
+// v_and_or_b32 into v_and_b32 + v_or_b32 (19 instead of 15 VALU ops per word).  The
+// constants come from opaque moves, made once per kernel, that the compiler cannot fold.
+struct UnpackConsts {
+  uint32_t mask;   // 0x000F000F, in an SGPR
+  uint32_t magic;  // 0x64006400, in a VGPR
+};
+__device__ __forceinline__ UnpackConsts unpack_consts() {
+  UnpackConsts c;
+  asm("s_mov_b32 %0, 0x000f000f" : "=s"(c.mask));
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(c.magic));
+  return c;
+}
+
+template <int I>
+__device__ __forceinline__ half2_t nibble_pair(uint32_t w, const UnpackConsts& c) {
+  uint32_t v;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(v) : "v"(I ? (w >> (4 * I)) : w), "s"(c.mask), "v"(c.magic));
+  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  return bit_cast<half2_t>(v) - bias;
+}
+
+__device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2, const UnpackConsts& c) {
+  const half2_t p0 = nibble_pair<0>(w, c) * s2, p1 = nibble_pair<1>(w, c) * s2;
+  const half2_t p2 = nibble_pair<2>(w, c) * s2, p3 = nibble_pair<3>(w, c) * s2;
+  half8_t out = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+  return out;
+}
+
 // Wave64 sum with DPP row ops; the total lands in lane 63.
 //   quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum
 //   row_shr:4, row_shr:8: lane 15 of each 16-lane row holds the row sum

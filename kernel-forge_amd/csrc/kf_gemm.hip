@@ -1,172 +1,312 @@
 // INT4 dequant GEMM on the CDNA4 matrix cores (v_mfma_f32_16x16x32_f16).
 //
-// y[M, N] = x[M, K] @ W_hat^T with W_hat = fp16_rne(q * s) exactly as the
-// reference's tensor-core path dequantizes (dequant_gemm_tc_kernel.cuh:100-112),
-// fp32 accumulation, fp16 RNE output.  Optional split-K writes fp32 partials
-// that kf::splitk_reduce sums in fixed split order (deterministic), the
-// behaviour of the reference's splitk_reduce (dequant_gemm_tc_kernel.cuh:156-162).
+// y[M, N] = x[M, K] @ W_hat^T with W_hat = fp16_rne(q * s) exactly as the reference's
+// tensor-core path dequantizes (dequant_gemm_tc_kernel.cuh:100-112), fp32 accumulation,
+// fp16 RNE output.  Optional split-K writes fp32 partials that kf::splitk_reduce sums in
+// fixed split order (deterministic), the behaviour of the reference's splitk_reduce
+// (dequant_gemm_tc_kernel.cuh:156-162).
 //
-// Block tile BM x BN x 64 with 256 threads (4 wavefronts as WM x WN); each
-// wavefront owns a (BM/WM) x (BN/WN) accumulator tile of 16x16 MFMA blocks.
-// Per k-tile of 64 (64 <= G, so one scale per row and k-tile):
-//   global -> registers: x tile as dwordx4 (rows >= M zero-filled) and the
-//     packed tile as dwordx4 (32 B per weight row; rows >= N clamped to N-1);
-//   registers -> LDS: x stored as is; weights unpacked and scaled to fp16
-//     W_hat once per block (not once per wavefront) and stored row-major;
-//   LDS -> MFMA: lane l reads 8 consecutive k of row (l % 16) for both A (x)
-//     and B (W_hat) fragments, 16 B each, from rows padded to 72 halves.
-// The next k-tile's global loads are issued before the current tile's MFMAs.
+// Design (gfx950: 4 SIMDs per CU, ~2 VALU ops hide under one 16x16x32 MFMA, LDS reads
+// ~150-200 B/clk per CU):
+//   * Workgroup tile BM x BN; WGM x WGN wavefronts tile it, and WK such groups split each
+//     stage's k range (in-block split-K, summed in fixed order through LDS at the end).
+//   * A stage covers SK = 64 * WK k.  x is staged in LDS as fp16; the weights stay PACKED
+//     in LDS (4 bits per weight: 4x less LDS traffic than an fp16 W_hat tile).  Each
+//     wavefront dequantizes only its own columns, with one scale per column and stage, so
+//     a weight is dequantized once per (workgroup, M-wavefront row); with WGM = 1 that is
+//     once per workgroup.
+//   * Global -> registers two stages ahead, registers -> LDS one stage ahead, LDS double
+//     buffered: one barrier per stage.
+//   * LDS layouts are XOR-swizzled so every fragment read and tile write is free of bank
+//     conflicts on gfx950's 64-bank LDS: x rows are 16-byte chunks c stored at slot
+//     c ^ f(row); packed rows are 8-byte units u stored at u ^ f'(row).
+//   * MFMA operands: lane l serves row / column l % 16 and k-group g = l / 16.  In sub-step
+//     t (0, 1) of k-group kw it supplies k = 64 kw + 16 g + 8 t .. +7 for both A (one
+//     16-byte x chunk) and B (one packed word, dequantized with dequant8), so one 8-byte
+//     LDS read gives a lane both sub-steps' weights.
+//   * Tiles are ordered in bands of group_m M-tiles (all N-tiles of a band before the next
+//     band) and the bands are dealt to the 8 XCDs in contiguous runs, so the x rows an XCD
+//     uses stay in its L2 and each weight tile is fetched once per band.
+#include <type_traits>
+
 #include "kf_device.h"
 #include "kf_launch.h"
 
 namespace kf {
 namespace {
 
-constexpr int BK = 64;
-constexpr int LDS_STRIDE = BK + 8;  // halves per LDS row (144 B, 16 B aligned)
 constexpr int kXcds = 8;
 
-template <int BM, int BN, int WM, int WN, bool XCD_ORDER>
-__global__ __launch_bounds__(256) void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
-                                                   const half_t* __restrict__ scales, half_t* __restrict__ y,
-                                                   float* __restrict__ ws, int M, int N, int K, int log2_group,
-                                                   int kt_per_split, int tiles_n, int tiles_total) {
-  static_assert(WM * WN == 4, "256 threads = 4 wavefronts");
-  constexpr int TM = BM / WM / 16;
-  constexpr int TN = BN / WN / 16;
-  static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 16x16 block");
-  constexpr int A_VECS = BM * (BK / 8);  // dwordx4 per x tile
-  constexpr int B_VECS = BN * (BK / 32); // dwordx4 per packed tile
-  constexpr int A_PER_T = (A_VECS + 255) / 256;
-  constexpr int B_PER_T = (B_VECS + 255) / 256;
+template <int BM_, int BN_, int WGM_, int WGN_, int WK_, int WAVES_PER_SIMD_ = 2>
+struct TileCfg {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, WK = WK_;
+  // Occupancy target: 2 wavefronts per SIMD leave 256 registers per lane, 1 leaves 512.
+  static constexpr int WAVES_PER_SIMD = WAVES_PER_SIMD_;
+  static constexpr int THREADS = 64 * WGM * WGN * WK;
+  static constexpr int SK = 64 * WK;                  // k per stage
+  static constexpr int A_ROW = 2 * SK;                // bytes per x row in LDS
+  static constexpr int A_CHUNKS_ROW = SK / 8;         // 16-byte chunks per x row
+  static constexpr int B_ROW = SK / 2;                // bytes per packed row in LDS
+  static constexpr int B_CHUNKS_ROW = SK / 32;        // 16-byte chunks per packed row
+  static constexpr int B_UNITS_ROW = SK / 16;         // 8-byte units per packed row
+  static constexpr int A_STAGE = BM * A_ROW;
+  static constexpr int B_STAGE = BN * B_ROW;
+  static constexpr int S_STAGE = WK * BN * 2;         // fp16 scales [WK][BN]
+  static constexpr int STAGE = A_STAGE + B_STAGE + S_STAGE;
+  static constexpr int A_CHUNKS = BM * A_CHUNKS_ROW;
+  static constexpr int B_CHUNKS = BN * B_CHUNKS_ROW;
+  static constexpr int A_PER_T = A_CHUNKS / THREADS;
+  static constexpr int B_PER_T = (B_CHUNKS + THREADS - 1) / THREADS;
+  static constexpr int TM = BM / WGM / 16;            // 16x16 blocks per wavefront along M
+  static constexpr int TN = BN / WGN / 16;            // ... along N
+  static constexpr int RED = (WK - 1) * WGM * WGN * TM * TN * 256 * 4;  // bytes of k-group partials
+  static_assert(A_CHUNKS % THREADS == 0, "x tile must split evenly over the threads");
+  static_assert(TM >= 1 && TN >= 1 && BM % (16 * WGM) == 0 && BN % (16 * WGN) == 0, "wave tile");
+  static_assert(16 % B_UNITS_ROW == 0, "packed-row swizzle needs 4, 8 or 16 units per row");
+  static_assert(STAGE % 16 == 0, "stage alignment");
+  static_assert(RED <= 2 * STAGE, "k-group reduction must fit in the stage buffers");
+  static_assert(2 * STAGE <= 160 * 1024, "LDS");
+};
 
-  __shared__ __attribute__((aligned(16))) half_t As[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) half_t Bs[BN * LDS_STRIDE];
+// Swizzle of 8-byte units in packed row `row`: rows that a 16-lane phase of an 8-byte read
+// touches land on distinct banks.
+template <class C>
+__device__ __forceinline__ int b_swizzle(int row) {
+  return (row / (16 / C::B_UNITS_ROW)) & (C::B_UNITS_ROW - 1);
+}
+
+template <class C>
+struct StageRegs {
+  u32x4 a[C::A_PER_T];
+  u32x4 b[C::B_PER_T];
+  half_t s[C::B_PER_T];
+};
+
+template <class C>
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_SIMD, C::WAVES_PER_SIMD)))
+void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales,
+                 half_t* __restrict__ y, float* __restrict__ ws, int M, int N, int K, int log2_group,
+                 int stages_per_split, int tiles_m, int tiles_n, int group_m) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * C::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-  // Tile of this workgroup.  Consecutive workgroup ids rotate over the 8 XCDs;
-  // with XCD_ORDER each XCD takes a contiguous run of tiles (M-major), so the
-  // x rows and weight columns it touches stay in that XCD's L2.
-  const int bid = blockIdx.x;
-  int tile = bid;
-  if (XCD_ORDER) {
-    const int per_xcd = (tiles_total + kXcds - 1) / kXcds;
-    tile = (bid % kXcds) * per_xcd + bid / kXcds;
-  }
-  if (tile >= tiles_total) return;
-  const int tm = tile / tiles_n;
-  const int n0 = (tile - tm * tiles_n) * BN;
-  const int m0 = tm * BM;
-  const int nkt = K / BK;
-  const int kt_begin = blockIdx.y * kt_per_split;
-  const int kt_end = min(nkt, kt_begin + kt_per_split);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave / (C::WGM * C::WGN);
+  const int wmn = wave - kw * (C::WGM * C::WGN);
+  const int wm = wmn / C::WGN;
+  const int wn = wmn - wm * C::WGN;
+  const int g = lane >> 4;
+  const int l16 = lane & 15;
+
+  // Tile of this workgroup (see the header comment for the order).
+  const int total = tiles_m * tiles_n;
+  const int per_xcd = (total + kXcds - 1) / kXcds;
+  const int t = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (t >= total) return;
+  const int band = group_m * tiles_n;
+  const int bi = t / band;
+  const int tb = t - bi * band;
+  const int gm = min(group_m, tiles_m - bi * group_m);
+  const int mt = bi * group_m + tb % gm;
+  const int nt = tb / gm;
+  const int m0 = mt * C::BM;
+  const int n0 = nt * C::BN;
+
+  const int nst = K / C::SK;
+  const int st_begin = blockIdx.y * stages_per_split;
+  const int st_end = min(nst, st_begin + stages_per_split);
+  const int ns = st_end - st_begin;
   const int words_per_row = K >> 3;
   const int groups_per_row = K >> log2_group;
 
-  u32x4 areg[A_PER_T];
-  u32x4 breg[B_PER_T];
-  half_t sreg[B_PER_T];
-
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * BK;
+  // Global -> registers.  Rows of x past M are clamped (they only feed output rows that
+  // are never stored); weight rows past N are clamped the same way.  Every thread loads
+  // every stage unconditionally (stage indices are clamped instead), which keeps the
+  // compiler's per-register load tracking exact: a wait covers only the stage it needs.
+  const half_t* a_src[C::A_PER_T];
 #pragma unroll
-    for (int j = 0; j < A_PER_T; ++j) {
-      const int i = tid + 256 * j;
-      if (A_VECS % 256 == 0 || i < A_VECS) {
-        const int row = i >> 3, c = i & 7;
-        const int m = m0 + row;
-        if (m < M) {
-          areg[j] = load_u32x4(x + (size_t)m * K + k0 + 8 * c);
-        } else {
-          areg[j] = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+  for (int j = 0; j < C::A_PER_T; ++j) {
+    const int i = tid + C::THREADS * j;
+    const int row = i / C::A_CHUNKS_ROW, c = i % C::A_CHUNKS_ROW;
+    a_src[j] = x + (size_t)min(m0 + row, M - 1) * K + 8 * c;
+  }
+  const uint32_t* b_src[C::B_PER_T];
+  const half_t* s_src[C::B_PER_T];
+#pragma unroll
+  for (int j = 0; j < C::B_PER_T; ++j) {
+    const int i = min(tid + C::THREADS * j, C::B_CHUNKS - 1);
+    const int row = i / C::B_CHUNKS_ROW, h = i % C::B_CHUNKS_ROW;
+    const int n = min(n0 + row, N - 1);
+    b_src[j] = packed + (size_t)n * words_per_row + 4 * h;
+    s_src[j] = scales + (size_t)n * groups_per_row;
+  }
+  auto load = [&](StageRegs<C>& R, int st) {
+    const int k0 = st * C::SK;
+#pragma unroll
+    for (int j = 0; j < C::A_PER_T; ++j) R.a[j] = load_u32x4(a_src[j] + k0);
+#pragma unroll
+    for (int j = 0; j < C::B_PER_T; ++j) {
+      const int h = (tid + C::THREADS * j) % C::B_CHUNKS_ROW;
+      R.b[j] = load_u32x4(b_src[j] + (k0 >> 3));
+      R.s[j] = s_src[j][(k0 + 32 * (h & ~1)) >> log2_group];
+    }
+  };
+
+  // x tile: 16-byte chunk c of row r sits at slot c ^ a_swizzle(r).  Sixteen consecutive
+  // rows (one 16-lane phase of a 16-byte read) then cover all 64 banks.
+  auto a_slot = [](int row, int c) {
+    constexpr int RSH = C::A_ROW >= 256 ? 0 : 1;  // rows per 256-byte bank window: 1 or 2
+    return c ^ ((row >> RSH) & (C::A_CHUNKS_ROW - 1));
+  };
+
+  // Registers -> LDS stage buffer (swizzled).
+  auto store = [&](const StageRegs<C>& R, unsigned char* st) {
+#pragma unroll
+    for (int j = 0; j < C::A_PER_T; ++j) {
+      const int i = tid + C::THREADS * j;
+      const int row = i / C::A_CHUNKS_ROW, c = i % C::A_CHUNKS_ROW;
+      *reinterpret_cast<u32x4*>(st + row * C::A_ROW + 16 * a_slot(row, c)) = R.a[j];
     }
 #pragma unroll
-    for (int j = 0; j < B_PER_T; ++j) {
-      const int i = tid + 256 * j;
-      if (B_VECS % 256 == 0 || i < B_VECS) {
-        const int row = i >> 1, h = i & 1;
-        const int n = min(n0 + row, N - 1);
-        breg[j] = load_u32x4_stream(packed + (size_t)n * words_per_row + (k0 >> 3) + 4 * h);
-        sreg[j] = scales[(size_t)n * groups_per_row + (k0 >> log2_group)];
+    for (int j = 0; j < C::B_PER_T; ++j) {
+      const int i = tid + C::THREADS * j;
+      if (C::B_CHUNKS % C::THREADS == 0 || i < C::B_CHUNKS) {
+        const int row = i / C::B_CHUNKS_ROW, h = i % C::B_CHUNKS_ROW;
+        const int sw = b_swizzle<C>(row);
+        unsigned char* rb = st + C::A_STAGE + row * C::B_ROW;
+        *reinterpret_cast<uint2*>(rb + 8 * ((2 * h) ^ sw)) = uint2{R.b[j].x, R.b[j].y};
+        *reinterpret_cast<uint2*>(rb + 8 * ((2 * h + 1) ^ sw)) = uint2{R.b[j].z, R.b[j].w};
+        if ((h & 1) == 0)
+          reinterpret_cast<half_t*>(st + C::A_STAGE + C::B_STAGE)[(h >> 1) * C::BN + row] = R.s[j];
       }
     }
   };
 
-  auto store_tile = [&]() {
+  float4_t acc[C::TM][C::TN];
 #pragma unroll
-    for (int j = 0; j < A_PER_T; ++j) {
-      const int i = tid + 256 * j;
-      if (A_VECS % 256 == 0 || i < A_VECS) {
-        const int row = i >> 3, c = i & 7;
-        *reinterpret_cast<u32x4*>(&As[row * LDS_STRIDE + 8 * c]) = areg[j];
-      }
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Packed words (both sub-steps) and scales of this wave's columns for one stage.
+  uint2 bw[C::TN];
+  half2_t s2[C::TN];
+  auto read_b = [&](const unsigned char* st) {
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int row = (wn * C::TN + j) * 16 + l16;
+      const int u = 4 * kw + g;
+      bw[j] = *reinterpret_cast<const uint2*>(st + C::A_STAGE + row * C::B_ROW + 8 * (u ^ b_swizzle<C>(row)));
+      const half_t sc = reinterpret_cast<const half_t*>(st + C::A_STAGE + C::B_STAGE)[kw * C::BN + row];
+      s2[j] = half2_t{sc, sc};
     }
+  };
+  auto read_a = [&](const unsigned char* st, int sub, half8_t (&a)[C::TM]) {
 #pragma unroll
-    for (int j = 0; j < B_PER_T; ++j) {
-      const int i = tid + 256 * j;
-      if (B_VECS % 256 == 0 || i < B_VECS) {
-        const int row = i >> 1, h = i & 1;
-        const half2_t s2 = {sreg[j], sreg[j]};
+    for (int i = 0; i < C::TM; ++i) {
+      const int row = (wm * C::TM + i) * 16 + l16;
+      a[i] = *reinterpret_cast<const half8_t*>(st + row * C::A_ROW + 16 * a_slot(row, 8 * kw + 2 * g + sub));
+    }
+  };
+  auto mfma_sub = [&](const half8_t (&a)[C::TM], const uint32_t (&w)[C::TN], const half2_t (&sc)[C::TN]) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-          *reinterpret_cast<half8_t*>(&Bs[row * LDS_STRIDE + 32 * h + 8 * w]) = dequant8(breg[j][w], s2);
-      }
+    for (int j = 0; j < C::TN; ++j) {
+      const half8_t b = dequant8(w[j], sc[j]);
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[i][j], 0, 0, 0);
     }
   };
 
-  float4_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int frag_row = lane & 15;
-  const int frag_k = (lane >> 4) * 8;
-
-  if (kt_begin < kt_end) load_tile(kt_begin);
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    __syncthreads();  // every wavefront is done reading the previous tile
-    store_tile();
+  // Software pipeline, one barrier per stage.  Stage s lives in LDS buffer s % 2 and is
+  // computed in two sub-steps; the LDS reads for the next sub-step are issued before the
+  // MFMAs of the current one, and the barrier sits between the two sub-steps:
+  //   read x(sub 1) | MFMA sub 0 | write stage s+1 to the other buffer, load stage s+3 |
+  //   barrier | read words, scales, x(sub 0) of stage s+1 | MFMA sub 1
+  // Registers R[(s+1) % 2] carry stage s+1 from global memory to LDS (loaded two stages
+  // ahead).  Stage indices past the split's end are clamped to its last stage; those
+  // duplicate loads, writes and reads are never used.
+  unsigned char* const L0 = smem;
+  unsigned char* const L1 = smem + C::STAGE;
+  const int last = st_end - 1;
+  auto stage_at = [&](int i) { return min(st_begin + i, last); };
+  StageRegs<C> R0, R1;
+  half8_t a0[C::TM], a1[C::TM];
+  if (ns > 0) {
+    load(R0, stage_at(0));
+    load(R1, stage_at(1));
+    store(R0, L0);
+    load(R0, stage_at(2));
     __syncthreads();
-    if (kt + 1 < kt_end) load_tile(kt + 1);
+    read_b(L0);
+    read_a(L0, 0, a0);
+
+    auto half_iter = [&](auto cur_c, int s) {
+      constexpr int CUR = decltype(cur_c)::value;
+      unsigned char* const cur = CUR ? L1 : L0;
+      unsigned char* const nxt = CUR ? L0 : L1;
+      StageRegs<C>& Rn = CUR ? R0 : R1;
+      uint32_t w0[C::TN], w1[C::TN];
+      half2_t sc[C::TN];
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      half8_t a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        a[i] = *reinterpret_cast<const half8_t*>(
-            &As[((wm * TM + i) * 16 + frag_row) * LDS_STRIDE + 32 * ks + frag_k]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        b[j] = *reinterpret_cast<const half8_t*>(
-            &Bs[((wn * TN + j) * 16 + frag_row) * LDS_STRIDE + 32 * ks + frag_k]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < C::TN; ++j) {
+        w0[j] = bw[j].x;
+        w1[j] = bw[j].y;
+        sc[j] = s2[j];
+      }
+      read_a(cur, 1, a1);
+      mfma_sub(a0, w0, sc);
+      store(Rn, nxt);
+      load(Rn, stage_at(s + 3));
+      __syncthreads();
+      read_b(nxt);
+      read_a(nxt, 0, a0);
+      mfma_sub(a1, w1, sc);
+    };
+    for (int s = 0; s < ns; s += 2) {
+      half_iter(std::integral_constant<int, 0>(), s);
+      if (s + 1 >= ns) break;
+      half_iter(std::integral_constant<int, 1>(), s + 1);
     }
+  }
+  __syncthreads();
+
+  // In-block split-K: k-groups 1.. hand their partial tiles to k-group 0 through LDS (the
+  // stage buffers are free after the barrier above) and it adds them in fixed order.
+  if constexpr (C::WK > 1) {
+    float* red = reinterpret_cast<float*>(smem);
+    constexpr int WAVE_FLOATS = C::TM * C::TN * 256;
+    if (kw > 0) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          *reinterpret_cast<float4_t*>(
+              &red[((kw - 1) * C::WGM * C::WGN + wmn) * WAVE_FLOATS + (i * C::TN + j) * 256 + 4 * lane]) = acc[i][j];
+    }
+    __syncthreads();
+    if (kw > 0) return;
+#pragma unroll
+    for (int q = 1; q < C::WK; ++q)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] += *reinterpret_cast<const float4_t*>(
+              &red[((q - 1) * C::WGM * C::WGN + wmn) * WAVE_FLOATS + (i * C::TN + j) * 256 + 4 * lane]);
   }
 
   // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
-  const int out_col = lane & 15;
-  const int out_row = (lane >> 4) * 4;
   float* part = ws ? ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + (wn * TN + j) * 16 + out_col;
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = n0 + (wn * C::TN + j) * 16 + l16;
       if (col >= N) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + (wm * TM + i) * 16 + out_row + r;
+        const int row = m0 + (wm * C::TM + i) * 16 + 4 * g + r;
         if (row < M) {
           if (part)
             part[(size_t)row * N + col] = acc[i][j][r];
@@ -175,6 +315,263 @@ __global__ __launch_bounds__(256) void gemm_kernel(const half_t* __restrict__ x,
         }
       }
     }
+}
+
+// ---- DMA-fed kernel: 128 x 128 tile, 4 wavefronts, 64-k stages ------------------------
+//
+// Every byte of a stage goes global -> LDS through the gfx950 LDS-DMA loads
+// (global_load_lds_dwordx4 / _ushort: lane l's data lands at M0 + 16 l, or M0 + 4 l for
+// 16-bit loads, zero-extended), so staging costs no registers and no VALU/LDS-write
+// instructions, and the 128 accumulators per lane of a 128 x 64 wave tile fit with two
+// wavefronts per SIMD.  A 128 x 64 wave tile makes one dequantized weight fragment feed 8
+// MFMAs (the VALU work stays under the MFMA shadow) and one x fragment feed 4 (LDS reads
+// stay well under the LDS bandwidth).
+//
+// Wavefront (kw, wn): column half wn (64 columns) and k-group kw, which takes k 32 kw ..
+// 32 kw + 31 of every 64-k stage; the two k-groups' accumulators are summed in fixed order
+// through LDS at the end (in-block split-K).  Four wavefronts per 128 x 128 tile keep the
+// number of equal wave tasks high enough to spread evenly over the 1024 SIMDs.
+//
+// The DMA loads are issued from inline assembly with a "memory" clobber: the compiler
+// neither tracks them nor moves LDS accesses across them, and the loop contains no
+// compiler-tracked global loads, so its own waits never cover the prefetches.  Each
+// wavefront issues exactly kDmaPerStage loads per stage (stage indices are clamped, never
+// skipped), so "s_waitcnt vmcnt(kDmaPerStage)" means: the older stage has landed, the
+// newer one may still be in flight.
+//
+// LDS stage layout (bytes): x rows of 128 B (64 k) with 16-byte chunk c at slot
+// c ^ ((row >> 1) & 7); packed rows of 32 B with 16-byte half h at h ^ ((row >> 3) & 1).
+// Every read phase of the MFMA fragments is free of bank conflicts.  Three stages rotate.
+// Scales change once per group (G >= 64 = one stage), so they live in their own ring of
+// three slabs of 4-byte slots, one slab per group, fetched by the k-group 0 wavefronts with
+// the first stage of the group: a stage that starts a group costs those two wavefronts one
+// more DMA, and their wait count for it is one higher.
+namespace dma {
+constexpr int BM = 128, BN = 128, BK = 64, NS = 3, THREADS = 256;
+constexpr int TM = 8, TN = 4;
+constexpr int A_ROW = BK * 2;              // 128 B
+constexpr int A_BYTES = BM * A_ROW;        // 16384
+constexpr int B_OFF = A_BYTES;
+constexpr int B_ROW = BK / 2;              // 32 B
+constexpr int B_BYTES = BN * B_ROW;        // 4096
+constexpr int STAGE = B_OFF + B_BYTES;     // 20480
+constexpr int S_RING = NS * STAGE;         // scale slabs after the stages: [NS][BN] 4-byte slots
+constexpr int S_SLAB = BN * 4;
+constexpr int OUT_ROW = BN * 2 + 16;       // epilogue fp16 tile row stride (bytes), padded
+constexpr int RED_BYTES = 2 * TM * TN * 256 * 4;  // k-group 1's partial tiles (2 wavefronts)
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int SMEM = cmax(cmax(S_RING + NS * S_SLAB, RED_BYTES), BM * OUT_ROW);  // epilogue reuses it
+constexpr int kDmaPerStage = 5;            // per wavefront: 4 x, 1 packed (+1 scales, see below)
+}  // namespace dma
+
+__device__ __forceinline__ void dma_16B(uint32_t lds, const void* src) {
+  asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lds), "v"(src) : "memory");
+}
+__device__ __forceinline__ void dma_u16(uint32_t lds, const void* src) {
+  asm volatile("global_load_lds_ushort %1, off" ::"{m0}"(lds), "v"(src) : "memory");
+}
+
+__global__ __launch_bounds__(dma::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
+                     const half_t* __restrict__ scales, half_t* __restrict__ y, float* __restrict__ ws, int M, int N,
+                     int K, int log2_group, int stages_per_split, int tiles_m, int tiles_n, int group_m) {
+  using namespace dma;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1;
+  const int kw = wave >> 1;
+  const int g = lane >> 4;
+  const int l16 = lane & 15;
+
+  const int total = tiles_m * tiles_n;
+  const int per_xcd = (total + kXcds - 1) / kXcds;
+  const int t = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (t >= total) return;
+  const int band = group_m * tiles_n;
+  const int bi = t / band;
+  const int tb = t - bi * band;
+  const int gm = min(group_m, tiles_m - bi * group_m);
+  const int m0 = (bi * group_m + tb % gm) * BM;
+  const int n0 = (tb / gm) * BN;
+
+  const int nst = K / BK;
+  const int st_begin = blockIdx.y * stages_per_split;
+  const int last = min(nst, st_begin + stages_per_split) - 1;
+  const int ns = last + 1 - st_begin;
+
+  // Per-lane DMA sources at k = 0 (advanced by the stage's k offset).  x: this wave's 4
+  // instructions cover rows 32 wave .. +31, 8 rows each, 8 lanes per row.  packed: rows
+  // 32 wave .. +31, 2 lanes per row.  scales: column 64 wn + lane, for k-group kw.
+  const half_t* a_src[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 8 * (4 * wave + q) + (lane >> 3);
+    a_src[q] = x + (size_t)min(m0 + row, M - 1) * K + 8 * ((lane & 7) ^ ((row >> 1) & 7));
+  }
+  const int brow = 32 * wave + (lane >> 1);
+  const uint32_t* b_src =
+      packed + (size_t)min(n0 + brow, N - 1) * (K >> 3) + 4 * ((lane & 1) ^ ((brow >> 3) & 1));
+  const half_t* s_src = scales + (size_t)min(n0 + 64 * wn + lane, N - 1) * (K >> log2_group);
+  const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
+
+  // Split-local stage i (clamped) starts a scale group when i == 0 or its k0 is a multiple
+  // of G; groups are numbered from the split's first stage.  The clamped repeats of the
+  // last stage past the split's end never start one.
+  const int log2_spg = log2_group - 6;  // log2(stages per group)
+  auto starts_group = [&](int i) {
+    const int st = st_begin + i;
+    return i == 0 || (st <= last && (st & ((1 << log2_spg) - 1)) == 0);
+  };
+  auto group_of = [&](int i) {  // split-local group index of split-local stage i (i <= ns - 1)
+    return ((st_begin + i) >> log2_spg) - (st_begin >> log2_spg);
+  };
+  // DMA of split-local stage i (clamped) into buffer i % NS, plus its group's scales.
+  // Returns whether this wavefront issued the scale load (one more outstanding load).
+  auto issue = [&](int i, int buf) {  // buf == i % NS
+    const int st = min(st_begin + i, last);
+    const int k0 = st * BK;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)(buf * STAGE));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_16B(base + 1024 * (4 * wave + q), a_src[q] + k0);
+    dma_16B(base + B_OFF + 1024 * wave, b_src + (k0 >> 3));
+    const bool sc = kw == 0 && starts_group(i);
+    if (sc) {
+      const uint32_t sbase =
+          __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)(S_RING + (group_of(i) % NS) * S_SLAB + 256 * wn));
+      dma_u16(sbase, s_src + (k0 >> log2_group));
+    }
+    return sc;
+  };
+  auto wait_older = [&](bool newer_has_scales) {  // all but the newest stage's loads landed
+    if (newer_has_scales)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerStage + 1) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerStage) : "memory");
+  };
+
+  float4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Lane-dependent LDS offsets inside a stage.  x: row l16 (+16 per block), chunk 4 kw + g.
+  // packed: row 64 wn + 16 j + l16, dword 4 kw + g.  scales: [kw][64 wn + 16 j + l16].
+  const int a_off = l16 * A_ROW + 16 * ((4 * kw + g) ^ ((l16 >> 1) & 7));
+  const int b_off = B_OFF + (64 * wn + l16) * B_ROW + 16 * (kw ^ ((l16 >> 3) & 1)) + 4 * g;
+  const int s_off = 4 * (64 * wn + l16);  // within a scale slab
+
+  const UnpackConsts uc = unpack_consts();
+  half8_t a[TM];
+  uint32_t w[TN];
+  half2_t s2[TN];
+  auto read_frags = [&](int i, int buf) {  // buf == i % NS, a compile-time constant at the call
+    const unsigned char* st = smem + buf * STAGE;
+    const unsigned char* slab = smem + S_RING + (group_of(i) % NS) * S_SLAB;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      w[j] = *reinterpret_cast<const uint32_t*>(st + b_off + 16 * B_ROW * j);
+      const half_t sc = *reinterpret_cast<const half_t*>(slab + s_off + 64 * j);
+      s2[j] = half2_t{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < TM; ++q) a[q] = *reinterpret_cast<const half8_t*>(st + a_off + 16 * A_ROW * q);
+  };
+
+  // Stage i: DMA issued at iteration i - 2 into buffer i % NS; at iteration i - 1 each
+  // wavefront waits for its own loads of it and the barrier publishes it; at iteration i
+  // its fragments are read and its MFMAs run.  The DMA of stage i + 2 (iteration i)
+  // overwrites the buffer of stage i - 1, whose reads completed before the barrier of
+  // iteration i - 1 (lgkmcnt(0) precedes every barrier).  Likewise the scale slab of group
+  // q is fetched with q's first stage i (iteration i - 2) into the slab of group q - 3,
+  // last read at a stage <= i - 3 (groups span >= 1 stage), before that barrier.
+  // The loop is unrolled by NS so every buffer offset is a compile-time immediate.
+  issue(0, 0);
+  wait_older(issue(1, 1));
+  __syncthreads();
+  auto step = [&](auto buf_c, int s) {  // stage s, held in buffer CUR == s % NS
+    constexpr int CUR = decltype(buf_c)::value;
+    read_frags(s, CUR);
+    wait_older(issue(s + 2, (CUR + 2) % NS));  // stage s + 1 landed
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const half8_t b = dequant8(w[j], s2[j], uc);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[i][j], 0, 0, 0);
+    }
+  };
+  static_assert(NS == 3, "the unrolled loop below assumes three stages");
+  for (int s = 0; s < ns; s += NS) {
+    step(std::integral_constant<int, 0>(), s);
+    if (s + 1 >= ns) break;
+    step(std::integral_constant<int, 1>(), s + 1);
+    if (s + 2 >= ns) break;
+    step(std::integral_constant<int, 2>(), s + 2);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped tail loads, before LDS is reused
+  __syncthreads();
+
+  // k-group 1 hands its partial tiles to k-group 0, which adds them (fixed order).
+  float* red = reinterpret_cast<float*>(smem);
+  if (kw == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<float4_t*>(&red[((wn * TM + i) * TN + j) * 256 + 4 * lane]) = acc[i][j];
+  }
+  __syncthreads();
+  if (kw == 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] += *reinterpret_cast<const float4_t*>(&red[((wn * TM + i) * TN + j) * 256 + 4 * lane]);
+  }
+
+  // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
+  if (ws) {
+    if (kw == 0) {
+      float* part = ws + (size_t)blockIdx.y * M * N;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = n0 + 64 * wn + 16 * j + l16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + 16 * i + 4 * g + r;
+            if (row < M && col < N) part[(size_t)row * N + col] = acc[i][j][r];
+          }
+        }
+    }
+    return;
+  }
+  // fp16 tile through LDS, then 16-byte row-major stores by all four wavefronts.
+  __syncthreads();  // the partial tiles have been read
+  if (kw == 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<half_t*>(smem + (16 * i + 4 * g + r) * OUT_ROW + 2 * (64 * wn + 16 * j + l16)) =
+              (half_t)acc[i][j][r];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < BM * BN / 8 / THREADS; ++q) {
+    const int c = tid + THREADS * q;
+    const int row = c >> 4, chunk = c & 15;
+    const int gr = m0 + row, gc = n0 + 8 * chunk;
+    if (gr < M && gc < N)
+      *reinterpret_cast<u32x4*>(y + (size_t)gr * N + gc) = *reinterpret_cast<const u32x4*>(smem + row * OUT_ROW + 16 * chunk);
+  }
 }
 
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, half_t* __restrict__ y,
@@ -186,28 +583,31 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
   }
 }
 
-struct TileCfg {
-  int bm, bn;
-  bool xcd;
-};
-// Tile table: index = GemmPlan::tile.
-constexpr TileCfg kTiles[] = {{16, 128, false}, {32, 128, false}, {64, 128, false}, {128, 128, false},
-                              {128, 128, true}, {64, 128, true}};
-constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-
 typedef void (*GemmFn)(const half_t*, const uint32_t*, const half_t*, half_t*, float*, int, int, int, int, int, int,
-                       int);
+                       int, int);
 
-GemmFn gemm_fn(int tile) {
-  switch (tile) {
-    case 0: return gemm_kernel<16, 128, 1, 4, false>;
-    case 1: return gemm_kernel<32, 128, 1, 4, false>;
-    case 2: return gemm_kernel<64, 128, 2, 2, false>;
-    case 3: return gemm_kernel<128, 128, 2, 2, false>;
-    case 4: return gemm_kernel<128, 128, 2, 2, true>;
-    default: return gemm_kernel<64, 128, 2, 2, true>;
-  }
+struct TileEntry {
+  int bm, bn, sk, threads;  // tile, k per stage, workgroup size
+  GemmFn fn;
+};
+
+template <class C>
+TileEntry entry() {
+  return TileEntry{C::BM, C::BN, C::SK, C::THREADS, gemm_kernel<C>};
 }
+
+// Tile table: index = GemmPlan::tile.
+const TileEntry kTiles[] = {
+    entry<TileCfg<64, 128, 1, 4, 1>>(),   // 0: M <= 64
+    entry<TileCfg<128, 128, 1, 4, 1>>(),  // 1: wave 128x32
+    entry<TileCfg<128, 128, 1, 4, 2>>(),  // 2: same, 8 wavefronts splitting each 128-k stage
+    entry<TileCfg<128, 128, 2, 2, 1>>(),  // 3: wave 64x64
+    entry<TileCfg<128, 256, 1, 4, 1, 1>>(),  // 4: wave 128x64, one wavefront per SIMD
+    entry<TileCfg<64, 128, 1, 4, 2>>(),   // 5: M <= 64, 8 wavefronts
+    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, gemm_dma_kernel},  // 6: DMA-fed
+};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+constexpr int kDmaTile = 6;
 
 }  // namespace
 
@@ -217,21 +617,22 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
   GemmPlan p;
   p.skinny = false;
   p.sk = SkinnyPlan{0, 0, 0};
+  if (K % kTiles[tile].sk != 0) tile = tile == 5 ? 0 : 1;  // stage must divide K
   p.tile = tile;
   p.block_m = kTiles[tile].bm;
   p.block_n = kTiles[tile].bn;
-  const int nkt = K / BK;
+  const int nst = K / kTiles[tile].sk;
   const long tiles = (long)ceil_div(N, p.block_n) * ceil_div(M, p.block_m);
-  const long want = 2L * (cu_count > 0 ? cu_count : 256);
+  const long want = cu_count > 0 ? cu_count : 256;
   int splits = 1;
   if (tiles < want) {
     splits = (int)((want + tiles - 1) / tiles);
-    const int max_splits = nkt / 4 > 0 ? nkt / 4 : 1;  // at least 4 k-tiles per split
+    const int max_splits = nst / 4 > 0 ? nst / 4 : 1;  // at least 4 stages per split
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
   }
-  p.kt_per_split = ceil_div(nkt, splits);
-  p.splits = ceil_div(nkt, p.kt_per_split);  // no empty splits
+  p.kt_per_split = ceil_div(nst, splits);
+  p.splits = ceil_div(nst, p.kt_per_split);  // no empty splits
   return p;
 }
 
@@ -243,7 +644,9 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
     p.sk = skinny_plan(M, N, K, cu_count);
     return p;
   }
-  const int tile = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
+  // M <= 64: the 64-row tile; above, the DMA-fed 128 x 128 kernel (fastest measured on
+  // every TinyLlama-shaped layer at M = 128 .. 2048).
+  const int tile = M <= 64 ? 0 : kDmaTile;
   return gemm_plan_with_tile(M, N, K, cu_count, tile);
 }
 
@@ -254,14 +657,19 @@ size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
                        void* ws, int M, int N, int K, int group_size, hipStream_t stream) {
   if (p.skinny) return skinny_launch(p.sk, x, packed, scales, y, M, N, K, group_size, stream);
+  const TileEntry& e = kTiles[p.tile];
   const int log2_group = group_size == 128 ? 7 : 6;
-  const int tiles_n = ceil_div(N, p.block_n);
-  const int tiles_total = tiles_n * ceil_div(M, p.block_m);
-  const int grid_x = kTiles[p.tile].xcd ? ceil_div(tiles_total, kXcds) * kXcds : tiles_total;
+  const int tiles_m = ceil_div(M, e.bm);
+  const int tiles_n = ceil_div(N, e.bn);
+  const int total = tiles_m * tiles_n;
+  const int grid_x = ceil_div(total, kXcds) * kXcds;
+  // Bands of M-tiles: one band per XCD when the M-tiles divide evenly, else single rows.
+  int group_m = tiles_m / kXcds;
+  if (group_m < 1) group_m = 1;
   float* part = p.splits > 1 ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(gemm_fn(p.tile), dim3(grid_x, p.splits), dim3(256), 0, stream, static_cast<const half_t*>(x),
+  hipLaunchKernelGGL(e.fn, dim3(grid_x, p.splits), dim3(e.threads), 0, stream, static_cast<const half_t*>(x),
                      static_cast<const uint32_t*>(packed), static_cast<const half_t*>(scales),
-                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split, tiles_n, tiles_total);
+                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split, tiles_m, tiles_n, group_m);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const size_t mn = (size_t)M * N;

@@ -22,6 +22,14 @@ from kernelforge import _lib
 # (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
 # skinny MFMA kernel (M <= 32), then the tiled MFMA GEMM.
 GEMV_MAX_M = 3
+# The GEMV accepts every N for M <= 8 (as the reference's does); the MFMA kernels need
+# N % 64 == 0.  Between GEMV_MAX_M and this bound a shape the GEMM cannot take stays on
+# the GEMV, so int4_matmul accepts exactly what the reference's accepts.
+_GEMV_LIMIT_M = 8
+
+
+def _use_gemv(m: int, n: int) -> bool:
+    return m <= GEMV_MAX_M or (m <= _GEMV_LIMIT_M and n % 64 != 0)
 
 
 def _stream_ptr(device: torch.device) -> int:
@@ -115,10 +123,10 @@ def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group
 def int4_matmul(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """y = x @ W_hat^T for INT4 weights from kernelforge.quantize, choosing the kernel by M.
 
-    M <= GEMV_MAX_M: the bandwidth-bound GEMV; larger M: the MFMA GEMM.
-    Reference kernelforge/ops.py:204-214.
+    M <= GEMV_MAX_M: the bandwidth-bound GEMV; larger M: the MFMA GEMM (M <= 8 with N not
+    a multiple of 64 stays on the GEMV).  Reference kernelforge/ops.py:204-214.
     """
-    if x.shape[0] <= GEMV_MAX_M:
+    if _use_gemv(x.shape[0], packed.shape[0]):
         return int4_gemv(x, packed, scales, group_size)
     return int4_gemm(x, packed, scales, group_size)
 
@@ -197,8 +205,10 @@ def _(x, packed, scales, group_size):
 @torch.library.custom_op("kernelforge::int4_matmul_grouped", mutates_args=())
 def _int4_matmul_grouped_op(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
                             group_size: int) -> list[torch.Tensor]:
-    if xs[0].shape[0] <= GEMV_MAX_M:
+    if all(_use_gemv(x.shape[0], p.shape[0]) for x, p in zip(xs, packed)):
         return int4_gemv_grouped(xs, packed, scales, group_size)
+    if xs[0].shape[0] <= _GEMV_LIMIT_M:
+        return [int4_matmul(x, p, s, group_size) for x, p, s in zip(xs, packed, scales)]
     return [int4_gemm(x, p, s, group_size) for x, p, s in zip(xs, packed, scales)]
 
 

@@ -153,7 +153,7 @@ def test_grouped_gemv_bit_identical_to_single(error_log, m, group):
 
 
 @pytest.mark.parametrize("shapes,m_leads", [
-    ([(9, 256), (129, 512), (64, 4160), (1, 128)], [(1, 1), (2, 3)]),  # ragged N: GEMV sizes only
+    ([(9, 256), (129, 512), (64, 4160), (1, 128)], [(1, 1), (2, 3)]),  # ragged N at M <= 8: GEMV fallback
     ([(64, 256), (192, 512), (128, 4160)], [(2, 5), (33,)]),            # M > GEMV_MAX_M: per-problem GEMM
 ])
 def test_grouped_linear_ragged_and_bias(shapes, m_leads):
@@ -220,11 +220,11 @@ def test_gemm_rejects_n_not_multiple_of_64():
         ops.int4_gemm(x, dp, ds, 128)
 
 
-@pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, True), ("tinyllama_gate_up", 16, False),
-                                             ("tinyllama_down", 64, False)])
+@pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, True), ("tinyllama_down", 64, True),
+                                             ("tinyllama_gate_up", 16, False), ("tinyllama_gate_up", 768, False)])
 def test_gemm_is_deterministic(layer, m, splitk):
-    """Split-K partials (tiled GEMM) and the skinny kernel's per-wave K slices are reduced in
-    fixed order: repeated calls are bitwise identical."""
+    """Split-K partials, the DMA kernel's in-block k-group halves and the skinny kernel's
+    per-wave K slices are reduced in fixed order: repeated calls are bitwise identical."""
     n, k = LAYER_SHAPES[layer]
     _, _, dp, ds = _weights(n, k, 128)
     x = torch.from_numpy(_x(m, k, 99)).to(DEV)
