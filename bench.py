@@ -86,6 +86,7 @@ def parse_args():
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--no-e2e", action="store_true", help="skip the TinyLlama graph-decode leg (config 5)")
+    ap.add_argument("--no-quant", action="store_true", help="skip the on-device quantize leg")
     return ap.parse_args()
 
 
@@ -219,6 +220,12 @@ def _cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def _timed_ms(fn) -> float:
+    t0 = time.perf_counter()
+    fn()
+    return (time.perf_counter() - t0) * 1e3
 
 
 class GraphSteps:
@@ -451,6 +458,27 @@ def main() -> int:
                  "gate_frac_of_spec_peak": round(gate_tf / SPEC_FP16_TFLOPS, 4), "per_layer": per}
         log(f"M=2048 gate {gate_tf} TFLOPS; hipBLASLt fp16 peak {mfma_peak:.0f} TFLOPS")
 
+    # --- on-device quantize + pack of an fp32 gate weight (format producer) --------------------
+    quant = None
+    if not args.no_quant:
+        log("quantize leg")
+        qn, qk = 5632, 2048
+        in_bytes, out_bytes = qn * qk * 4, qn * qk // 2 + 2 * qn * (qk // GROUP)
+        qcopies = max(2, -(-(2 * MALL_BYTES) // in_bytes))
+        wq = [torch.randn(qn, qk, device="cuda") * 0.02 for _ in range(qcopies)]
+        gs = GraphSteps(torch, lambda r: ops.int4_quantize(wq[r], GROUP), qcopies)
+        ms = gs.event_avg_ms(4 * qcopies)
+        gbps = (in_bytes + out_bytes) / (ms * 1e-3) / 1e9
+        w_host = wq[0].cpu()
+        kq.quantize_weight(w_host, GROUP)
+        cpu_ms = statistics.median(_timed_ms(lambda: kq.quantize_weight(w_host, GROUP)) for _ in range(3))
+        quant = {"shape_NxK": [qn, qk], "dtype_in": "fp32", "group_size": GROUP, "bytes_per_call": in_bytes + out_bytes,
+                 "us": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                 "pct_of_measured_copy": round(100 * gbps / ceil["hbm_copy_gbps"], 1),
+                 "cpu_torch_quantize_ms": round(cpu_ms, 2), "cpu_threads": torch.get_num_threads()}
+        log(f"quantize {ms * 1e3:.1f} us -> {gbps:.0f} GB/s; torch on the CPU {cpu_ms:.1f} ms")
+        del wq, gs
+
     # --- config 5: end-to-end graph decode ------------------------------------------------------
     e2e = None
     if not args.no_e2e:
@@ -511,6 +539,7 @@ def main() -> int:
         "per_layer_m1": per_layer,
         "m2048": m2048,
         "e2e_decode": e2e,
+        "quantize": quant,
         "device": props.name, "cu_count": props.multi_processor_count,
     }
     print(json.dumps(line), flush=True)

@@ -99,6 +99,20 @@ int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
 int kf_int4_dequant_fp16(const void* packed, const void* scales, void* w_hat,
                          int N, int K, int group_size, void* stream);
 
+/* Element types of a weight matrix handed to kf_int4_quantize. */
+#define KF_DTYPE_F32 0
+#define KF_DTYPE_F16 1
+#define KF_DTYPE_BF16 2
+
+/* Quantize and pack a weight matrix w [N, K] (row-major, dtype one of KF_DTYPE_*,
+ * 16-byte aligned, finite values) into packed int32 [N, K/8] and fp16 scales [N, K/G],
+ * bit for bit what quantize_weight() produces on the CPU: scale = fp16(max(absmax/7, 2^-14))
+ * (1 for an all-zero group), q = clamp(rint(w / scale), -8, 7), nibble order of
+ * pack_int4.  Replaces quantize_int4 + pack_int4 + quantize_weight
+ * (kernelforge/quantize.py:61-105), which run as torch elementwise ops. */
+int kf_int4_quantize(const void* w, int dtype, void* packed, void* scales,
+                     int N, int K, int group_size, void* stream);
+
 /* Streaming HBM ceilings with dwordx4 accesses: dst[i] = src[i] (copy),
  * a checksum of src folded into sink[0..grid) (read), dst[i] = pattern
  * (write).  bytes must be a multiple of 16.  grid_blocks <= 0 picks a default.

@@ -16,6 +16,8 @@
 #include "kf_int4.h"
 #include "kf_launch.h"
 
+static_assert(KF_DTYPE_F32 == kf::kQuantF32 && KF_DTYPE_F16 == kf::kQuantF16 && KF_DTYPE_BF16 == kf::kQuantBF16,
+              "dtype codes of the C ABI and the kernels differ");
 static_assert(KF_GEMV_MAX_GROUP == kf::kMaxGemvGroup, "header and kernels disagree on the group limit");
 
 namespace {
@@ -151,6 +153,23 @@ int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
   return hip_status(kf::gemm_launch(plan, x, packed, scales, y, ws, M, N, K, group_size,
                                     static_cast<hipStream_t>(stream)),
                     "int4_gemm launch");
+}
+
+int kf_int4_quantize(const void* w, int dtype, void* packed, void* scales, int N, int K, int group_size,
+                     void* stream) {
+  if (!w || !packed || !scales) return fail(KF_ERR_INVALID_ARG, "w, packed and scales must be non-null");
+  if (N < 1 || K < 1) return fail(KF_ERR_INVALID_ARG, "N, K must be positive, got N=%d K=%d", N, K);
+  if (group_size != 64 && group_size != 128)
+    return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);
+  if (K % group_size != 0)
+    return fail(KF_ERR_INVALID_ARG, "K=%d is not a multiple of group_size=%d. Pad K or pick another group size.", K,
+                group_size);
+  if (dtype != KF_DTYPE_F32 && dtype != KF_DTYPE_F16 && dtype != KF_DTYPE_BF16)
+    return fail(KF_ERR_INVALID_ARG, "dtype must be KF_DTYPE_F32, KF_DTYPE_F16 or KF_DTYPE_BF16, got %d", dtype);
+  if (!aligned(w, 16)) return fail(KF_ERR_INVALID_ARG, "w must be 16-byte aligned");
+  if (!aligned(packed, 4) || !aligned(scales, 2)) return fail(KF_ERR_INVALID_ARG, "packed / scales misaligned");
+  return hip_status(kf::quantize_launch(w, dtype, packed, scales, N, K, group_size, static_cast<hipStream_t>(stream)),
+                    "int4_quantize launch");
 }
 
 int kf_int4_dequant_fp16(const void* packed, const void* scales, void* w_hat, int N, int K, int group_size,

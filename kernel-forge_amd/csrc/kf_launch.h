@@ -76,6 +76,11 @@ size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N);
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
                        void* ws, int M, int N, int K, int group_size, hipStream_t stream);
 
+// ---- on-device quantize + pack (kf_quant.hip) -------------------------------
+constexpr int kQuantF32 = 0, kQuantF16 = 1, kQuantBF16 = 2;  // == KF_DTYPE_* of the C ABI
+hipError_t quantize_launch(const void* w, int dtype, void* packed, void* scales, int N, int K, int group_size,
+                           hipStream_t stream);
+
 // ---- auxiliary kernels ----------------------------------------------------
 hipError_t dequant_fp16_launch(const void* packed, const void* scales, void* w_hat, int N, int K, int group_size,
                                hipStream_t stream);

@@ -40,6 +40,7 @@ SIGNATURES = {
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
     "kf_int4_dequant_fp16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
+    "kf_int4_quantize": (_I, [_VP, _I, _VP, _VP, _I, _I, _I, _VP]),
     "kf_bw_copy": (_I, [_VP, _VP, _SZ, _I, _VP]),
     "kf_bw_read": (_I, [_VP, _VP, _SZ, _I, _VP]),
     "kf_bw_write": (_I, [_VP, _SZ, _I, _VP]),

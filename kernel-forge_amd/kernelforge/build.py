@@ -25,7 +25,7 @@ LIB_NAME = "libkf_int4.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
-SOURCES = ("kf_abi.hip", "kf_gemv.hip", "kf_gemm.hip", "kf_skinny.hip", "kf_aux.hip")
+SOURCES = ("kf_abi.hip", "kf_gemv.hip", "kf_gemm.hip", "kf_skinny.hip", "kf_quant.hip", "kf_aux.hip")
 
 # Packed fp32 VALU ops stay disabled: the kernels never need them and some of
 # their forms are not trusted on the target machines.  The first 16 dwords of

@@ -131,6 +131,41 @@ def int4_matmul(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, gro
     return int4_gemm(x, packed, scales, group_size)
 
 
+_QUANT_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}  # KF_DTYPE_* of the C ABI
+
+
+def int4_quantize(weight: torch.Tensor, group_size: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """(packed int32 [N, K/8], scales fp16 [N, K/G]) of a weight [N, K] on the GPU.
+
+    The gfx950 quantize + pack kernel; bit-identical to ``kernelforge.quantize.quantize_weight``
+    of the same weight on the CPU (the reference's quantize_int4 + pack_int4,
+    kernelforge/quantize.py:61-105).  fp32, fp16 or bf16 weights with finite values.
+    """
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D [N, K], got shape {tuple(weight.shape)}")
+    if group_size not in (64, 128):
+        raise ValueError(f"group_size must be one of (64, 128), got {group_size}")
+    n, k = weight.shape
+    if k % group_size:
+        raise ValueError(f"K={k} is not a multiple of group_size={group_size}. Pad K or pick another group size.")
+    if not weight.is_cuda:
+        raise TypeError("int4_quantize needs a CUDA tensor")
+    code = _QUANT_DTYPES.get(weight.dtype)
+    if code is None:
+        raise TypeError(f"int4_quantize supports float32, float16 and bfloat16 weights, got {weight.dtype}")
+    w = weight.contiguous()
+    if w.data_ptr() % 16:
+        w = w.clone()
+    lib = _lib.load()
+    packed = torch.empty(n, k // 8, dtype=torch.int32, device=w.device)
+    scales = torch.empty(n, k // group_size, dtype=torch.float16, device=w.device)
+    with torch.cuda.device(w.device):
+        status = lib.kf_int4_quantize(_ptr(w), code, _ptr(packed), _ptr(scales), n, k, int(group_size),
+                                      _stream_ptr(w.device))
+    _lib.check(status, "int4_quantize")
+    return packed, scales
+
+
 def int4_dequant_fp16(packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """W_hat = fp16(q * s) [N, K] on the GPU, the exact operand the GEMM feeds to the matrix cores.
 

@@ -17,8 +17,11 @@ Format (nn.Linear convention, W is [N, K] and y = x @ W^T):
   with 0x000F000F therefore leaves the pair (k 2i, k 2i+1) in the two 16-bit
   halves, which is what the GPU unpack relies on.
 
-This module is the offline format producer (it runs wherever the weight
-lives, with torch elementwise ops).  The GPU kernels never call it.
+This module is the format producer.  ``quantize_weight`` of a weight on a GPU
+runs the gfx950 quantize + pack kernel (``kernelforge.ops.int4_quantize``),
+bit-identical to the torch path below on the CPU; every other function runs
+wherever its tensor lives, with torch elementwise ops.  The GEMV/GEMM kernels
+never call this module.
 """
 
 from __future__ import annotations
@@ -105,9 +108,22 @@ def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
     return q.reshape(rows, words * 8)
 
 
+_KERNEL_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
 def quantize_weight(weight: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE) -> QuantizedWeight:
-    """Quantize and pack an nn.Linear weight [N, K]; reference quantize.py:100-105."""
+    """Quantize and pack an nn.Linear weight [N, K]; reference quantize.py:100-105.
+
+    A weight on a GPU in fp32 / fp16 / bf16 goes through the quantize kernel, which
+    divides exactly as the CPU does (torch's GPU division by the scalar 7 would multiply
+    by a rounded 1/7), so the result is the same bit for bit wherever the weight lives.
+    """
     rows, cols = _validate(weight, group_size)
+    if weight.is_cuda and weight.dtype in _KERNEL_DTYPES:
+        from kernelforge import ops  # deferred: ops loads the HIP library
+
+        packed, scales = ops.int4_quantize(weight, group_size)
+        return QuantizedWeight(packed=packed, scales=scales, group_size=group_size, shape=(rows, cols))
     q, scales = quantize_int4(weight, group_size)
     return QuantizedWeight(packed=pack_int4(q).contiguous(), scales=scales.contiguous(),
                            group_size=group_size, shape=(rows, cols))
