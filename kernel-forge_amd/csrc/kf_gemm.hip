@@ -636,17 +636,36 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
   return p;
 }
 
+// Kernel choice, from a sweep of every TinyLlama / Qwen2.5 layer shape over M = 16 .. 2048 on
+// MI355X (graph-replayed, weights read from HBM):
+//   * skinny: every shape up to M = 8; up to M = 16 when K <= 4096 (its per-wave K range grows
+//     with K), and up to M = 32 for small matrices (N*K <= 4.2M: TinyLlama q/o and k/v);
+//   * 64 x 128 with 8 wavefronts (tile 5): M <= 64, and N <= 4096 until the 128 x 128 grid fills
+//     the GPU;
+//   * 64 x 128 with 4 wavefronts (tile 0): wide N (gate/up) at M = 65 .. ~512;
+//   * DMA-fed 128 x 128: once it has a tile per CU, or K >= 8192 (long K amortizes its split-K).
 GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
-  if (M <= kSkinnyMaxM && K % 128 == 0) {
+  const int cus = cu_count > 0 ? cu_count : 256;
+  const bool k128 = K % 128 == 0;
+  if (M <= kSkinnyMaxM && k128 && (M <= 8 || (K <= 4096 && (M <= 16 || (long)N * K <= 4200000L)))) {
     GemmPlan p = gemm_plan_with_tile(M, N, K, cu_count, 0);
     p.skinny = true;
     p.splits = 1;
     p.sk = skinny_plan(M, N, K, cu_count);
     return p;
   }
-  // M <= 64: the 64-row tile; above, the DMA-fed 128 x 128 kernel (fastest measured on
-  // every TinyLlama-shaped layer at M = 128 .. 2048).
-  const int tile = M <= 64 ? 0 : kDmaTile;
+  int tile;
+  if (M <= 64) {
+    tile = k128 ? 5 : 0;
+  } else {
+    const long dma_tiles = (long)ceil_div(M, dma::BM) * ceil_div(N, dma::BN);
+    if (dma_tiles >= cus || (K >= 8192 && M > 128))
+      tile = kDmaTile;
+    else if (N >= 4096 || !k128)
+      tile = 0;
+    else
+      tile = 5;
+  }
   return gemm_plan_with_tile(M, N, K, cu_count, tile);
 }
 

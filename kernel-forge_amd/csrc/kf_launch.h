@@ -45,9 +45,8 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
                        hipStream_t stream);
 
-// ---- skinny MFMA GEMM (M <= 64, K % 128 == 0): one weight stream, K split in-block ----
-// Measured on MI355X (dispatch_sweep.py): at M=64 the tiled GEMM is faster on 4 of 6 shapes,
-// at M=32 the skinny kernel wins on 5 of 6.
+// ---- skinny MFMA GEMM (M <= 32, K % 128 == 0): one weight stream, K split in-block ----
+// gemm_plan (kf_gemm.hip) picks it for small M by the measured rule stated there.
 constexpr int kSkinnyMaxM = 32;
 struct SkinnyPlan {
   int m_tiles;   // 16-row tiles of M (1..4)

@@ -20,8 +20,8 @@ from kernelforge import _lib
 # Measured GEMV/GEMM crossover on one MI355X (kernelforge/dispatch_sweep.py): the
 # largest M at which the sum of GEMV times over the layer shapes beats the GEMM's
 # (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
-# skinny MFMA kernel (M <= 32), then the tiled MFMA GEMM.
-GEMV_MAX_M = 3
+# skinny MFMA kernel for small M, then the tiled MFMA kernels.
+GEMV_MAX_M = 2
 # The GEMV accepts every N for M <= 8 (as the reference's does); the MFMA kernels need
 # N % 64 == 0.  Between GEMV_MAX_M and this bound a shape the GEMM cannot take stays on
 # the GEMV, so int4_matmul accepts exactly what the reference's accepts.

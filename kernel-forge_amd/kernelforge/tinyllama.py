@@ -9,9 +9,10 @@ kernelforge/modules.py:51-65); embedding and lm_head stay fp16.
 
 ``fuse_decoder_linears_`` replaces q|k|v and gate|up by one INT4 module each whose packed rows are
 the concatenation of the originals (the packed format is per row, so this is the same format).
-For M <= 32 (decode and short prompts: the GEMV and skinny kernels, whose per-column arithmetic
-does not depend on N) the fused results are bit-identical; for larger M the tiled GEMM may pick a
-different split-K count for the wider matrix, which changes only the fp32 summation order.
+For M <= 16 (decode and short prompts: the GEMV and the skinny kernel, whose per-column
+arithmetic does not depend on N) the fused results are bit-identical; for larger M the fused and
+the separate matrices can take different tiled kernels or split-K counts, which changes only the
+fp32 summation order.
 
 Decode follows the reference's graph method (bench/e2e_model.py:85-141): static KV cache,
 positions in device tensors, one decode step captured in a HIP graph and replayed; the greedy
@@ -73,9 +74,9 @@ def _rotate_half(x: torch.Tensor) -> torch.Tensor:
 class FusedInt4Linear(nn.Module):
     """Several INT4 linears on the same input as ONE GEMV/GEMM over their concatenated rows.
 
-    Bit-identical to running them separately for M <= 32 (GEMV and skinny kernels compute each
-    column independently of N); above that the tiled GEMM's split-K count may differ, which only
-    reorders fp32 sums.  Returns the per-part outputs.
+    Bit-identical to running them separately for M <= 16 (GEMV and skinny kernels compute each
+    column independently of N); above that the tiled kernels' choice or split-K count may differ,
+    which only reorders fp32 sums.  Returns the per-part outputs.
     """
 
     def __init__(self, parts: list[KFLinearInt4]):
