@@ -1,0 +1,211 @@
+// Torch-free correctness workload for libkf_int4.so (test infrastructure).
+//
+// The counterpart of the reference's csrc/micro/sanitize_gemm.cu:31-95: the reference's LCG
+// inputs (restated in oracle/kf_oracle.c), the host packer, a double-precision reference, the
+// GEMV at every M <= 8 and the GEMM at every M (with split-K on these small grids), all through
+// the C ABI of include/kf_int4.h with plain HIP device memory: no torch, no Python.  It is
+// built twice by the package build: plainly and with AddressSanitizer on this host code.
+//
+// Checks: max|y - ref| <= 2e-3 * max|ref| (the reference's tolerance, tests/test_gemm.py:17),
+// bit-exact GPU dequantization, the ABI's status codes on bad arguments, and that a guard band
+// around y is never written.  Exit status 0 on success; one line per case on stdout.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "kf_int4.h"
+
+extern "C" {
+void kfo_lcg_workload(int group, int n, int k, const int* ms, int nms, int8_t* q, uint16_t* scales, int32_t* packed,
+                      uint16_t* xcat);
+void kfo_dequant_fp16(const int32_t* packed, const uint16_t* scales, int n, int k, int group, uint16_t* out);
+void kfo_ref_f64(const uint16_t* x, const int32_t* packed, const uint16_t* scales, int m, int n, int k, int group,
+                 double* y);
+float kfo_f16_to_f32(uint16_t h);
+}
+
+namespace {
+
+int g_failures = 0;
+
+void check(bool ok, const char* what) {
+  if (!ok) {
+    ++g_failures;
+    std::printf("FAIL %s\n", what);
+  }
+}
+
+bool hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    ++g_failures;
+    std::printf("FAIL %s: %s\n", what, hipGetErrorString(e));
+    return false;
+  }
+  return true;
+}
+
+// RAII device allocation (the role of the reference's DeviceBuffer, csrc/common/cuda_utils.cuh:18-50).
+class DeviceBuffer {
+ public:
+  explicit DeviceBuffer(size_t bytes) : bytes_(bytes) {
+    if (bytes_ && hipMalloc(&ptr_, bytes_) != hipSuccess) ptr_ = nullptr;
+  }
+  ~DeviceBuffer() {
+    if (ptr_) (void)hipFree(ptr_);
+  }
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  void* get() const { return ptr_; }
+  size_t bytes() const { return bytes_; }
+  bool upload(const void* src, size_t n) { return hipMemcpy(ptr_, src, n, hipMemcpyHostToDevice) == hipSuccess; }
+  bool download(void* dst, size_t n) const { return hipMemcpy(dst, ptr_, n, hipMemcpyDeviceToHost) == hipSuccess; }
+
+ private:
+  void* ptr_ = nullptr;
+  size_t bytes_;
+};
+
+// RAII hipEvent pair timing one region on a stream (the role of the reference's GpuTimer,
+// csrc/common/timer.cuh:14-75).
+class EventTimer {
+ public:
+  explicit EventTimer(hipStream_t s) : s_(s) {
+    (void)hipEventCreate(&a_);
+    (void)hipEventCreate(&b_);
+    (void)hipEventRecord(a_, s_);
+  }
+  ~EventTimer() {
+    (void)hipEventDestroy(a_);
+    (void)hipEventDestroy(b_);
+  }
+  float stop_us() {
+    float ms = 0.f;
+    (void)hipEventRecord(b_, s_);
+    (void)hipEventSynchronize(b_);
+    (void)hipEventElapsedTime(&ms, a_, b_);
+    return ms * 1e3f;
+  }
+
+ private:
+  hipStream_t s_;
+  hipEvent_t a_{}, b_{};
+};
+
+constexpr uint16_t kGuard = 0x7E11;  // an fp16 NaN pattern the kernels never produce
+constexpr int kGuardElems = 64;
+
+double max_rel_err(const std::vector<uint16_t>& y, const std::vector<double>& ref) {
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < ref.size(); ++i) {
+    num = std::fmax(num, std::fabs((double)kfo_f16_to_f32(y[i]) - ref[i]));
+    den = std::fmax(den, std::fabs(ref[i]));
+  }
+  return num / (den > 0.0 ? den : 1.0);
+}
+
+void run_group(int group, hipStream_t stream) {
+  const int n = 128, k = 1024;  // the reference's sizes (sanitize_gemm.cu:33-34)
+  const int ms[] = {1, 3, 8, 9, 16, 17, 33, 64, 65};
+  const int nms = sizeof(ms) / sizeof(ms[0]);
+  int msum = 0;
+  for (int m : ms) msum += m;
+  std::vector<int8_t> q((size_t)n * k);
+  std::vector<uint16_t> scales((size_t)n * (k / group)), xcat((size_t)msum * k);
+  std::vector<int32_t> packed((size_t)n * (k / 8));
+  kfo_lcg_workload(group, n, k, ms, nms, q.data(), scales.data(), packed.data(), xcat.data());
+
+  DeviceBuffer d_packed(packed.size() * 4), d_scales(scales.size() * 2);
+  if (!d_packed.get() || !d_scales.get()) return check(false, "hipMalloc weights");
+  check(d_packed.upload(packed.data(), d_packed.bytes()) && d_scales.upload(scales.data(), d_scales.bytes()),
+        "upload weights");
+
+  // Dequantization, bit for bit.
+  {
+    std::vector<uint16_t> want((size_t)n * k), got((size_t)n * k);
+    kfo_dequant_fp16(packed.data(), scales.data(), n, k, group, want.data());
+    DeviceBuffer d_w(got.size() * 2);
+    const int st = kf_int4_dequant_fp16(d_packed.get(), d_scales.get(), d_w.get(), n, k, group, stream);
+    check(st == KF_OK, kf_last_error());
+    hip_ok(hipStreamSynchronize(stream), "dequant sync");
+    check(d_w.download(got.data(), got.size() * 2), "download w_hat");
+    const bool same = std::memcmp(got.data(), want.data(), got.size() * 2) == 0;
+    std::printf("G=%d dequant_fp16 bit-exact=%d\n", group, (int)same);
+    check(same, "dequant_fp16 bit-exact");
+  }
+
+  size_t off = 0;
+  for (int m : ms) {
+    const uint16_t* x = xcat.data() + off;
+    off += (size_t)m * k;
+    std::vector<double> ref((size_t)m * n);
+    kfo_ref_f64(x, packed.data(), scales.data(), m, n, k, group, ref.data());
+    DeviceBuffer d_x((size_t)m * k * 2), d_y(((size_t)m * n + 2 * kGuardElems) * 2);
+    check(d_x.upload(x, d_x.bytes()), "upload x");
+    std::vector<uint16_t> guard((size_t)m * n + 2 * kGuardElems, kGuard);
+    uint16_t* y = static_cast<uint16_t*>(d_y.get()) + kGuardElems;
+
+    for (int path = 0; path < 2; ++path) {  // 0: GEMV (M <= 8), 1: GEMM
+      if (path == 0 && m > 8) continue;
+      check(d_y.upload(guard.data(), d_y.bytes()), "upload guard");
+      int st;
+      float us;
+      size_t ws_bytes = 0;
+      {
+        const size_t need = path ? kf_int4_gemm_workspace_bytes(m, n, k, group) : 0;
+        DeviceBuffer ws(need);
+        ws_bytes = need;
+        EventTimer t(stream);
+        st = path ? kf_int4_gemm(d_x.get(), d_packed.get(), d_scales.get(), y, ws.get(), need, m, n, k, group, stream)
+                  : kf_int4_gemv(d_x.get(), d_packed.get(), d_scales.get(), y, m, n, k, group, stream);
+        us = t.stop_us();
+        hip_ok(hipStreamSynchronize(stream), "kernel sync");
+      }
+      check(st == KF_OK, kf_last_error());
+      std::vector<uint16_t> all(guard.size());
+      check(d_y.download(all.data(), all.size() * 2), "download y");
+      bool guard_ok = true;
+      for (int i = 0; i < kGuardElems; ++i)
+        guard_ok &= all[i] == kGuard && all[all.size() - 1 - i] == kGuard;
+      std::vector<uint16_t> out(all.begin() + kGuardElems, all.end() - kGuardElems);
+      const double err = max_rel_err(out, ref);
+      std::printf("G=%d M=%d %s err=%.3e guard=%d ws=%zu time=%.1fus\n", group, m, path ? "gemm" : "gemv", err,
+                  (int)guard_ok, ws_bytes, us);
+      check(err <= 2e-3, "tolerance");
+      check(guard_ok, "guard band");
+    }
+  }
+}
+
+void run_rejections(hipStream_t stream) {
+  DeviceBuffer a(1 << 16), b(1 << 16), c(1 << 16), d(1 << 16);
+  int st = kf_int4_gemv(nullptr, b.get(), c.get(), d.get(), 1, 64, 256, 128, stream);
+  check(st == KF_ERR_INVALID_ARG, "null x rejected");
+  st = kf_int4_gemv(a.get(), b.get(), c.get(), d.get(), 1, 64, 256, 96, stream);
+  check(st == KF_ERR_INVALID_ARG && std::strstr(kf_last_error(), "group_size") != nullptr, "group 96 rejected");
+  st = kf_int4_gemm(a.get(), b.get(), c.get(), d.get(), nullptr, 0, 16, 100, 256, 128, stream);
+  check(st == KF_ERR_UNSUPPORTED, "gemm N % 64 rejected");
+  st = kf_int4_quantize(a.get(), 7, b.get(), c.get(), 16, 256, 128, stream);
+  check(st == KF_ERR_INVALID_ARG, "quantize dtype rejected");
+  std::printf("rejections checked\n");
+}
+
+}  // namespace
+
+int main() {
+  if (kf_abi_version() != KF_ABI_VERSION) {
+    std::printf("FAIL ABI version %d != %d\n", kf_abi_version(), KF_ABI_VERSION);
+    return 1;
+  }
+  hipStream_t stream;
+  if (!hip_ok(hipStreamCreate(&stream), "hipStreamCreate")) return 1;
+  run_group(64, stream);
+  run_group(128, stream);
+  run_rejections(stream);
+  (void)hipStreamDestroy(stream);
+  std::printf("%s (%d failures)\n", g_failures ? "FAILED" : "OK", g_failures);
+  return g_failures ? 1 : 0;
+}
