@@ -598,16 +598,12 @@ TileEntry entry() {
 
 // Tile table: index = GemmPlan::tile.
 const TileEntry kTiles[] = {
-    entry<TileCfg<64, 128, 1, 4, 1>>(),   // 0: M <= 64
-    entry<TileCfg<128, 128, 1, 4, 1>>(),  // 1: wave 128x32
-    entry<TileCfg<128, 128, 1, 4, 2>>(),  // 2: same, 8 wavefronts splitting each 128-k stage
-    entry<TileCfg<128, 128, 2, 2, 1>>(),  // 3: wave 64x64
-    entry<TileCfg<128, 256, 1, 4, 1, 1>>(),  // 4: wave 128x64, one wavefront per SIMD
-    entry<TileCfg<64, 128, 1, 4, 2>>(),   // 5: M <= 64, 8 wavefronts
-    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, gemm_dma_kernel},  // 6: DMA-fed
+    entry<TileCfg<64, 128, 1, 4, 1>>(),  // 0: 64 x 128, 4 wavefronts (wave 64 x 32)
+    entry<TileCfg<64, 128, 1, 4, 2>>(),  // 1: 64 x 128, 8 wavefronts splitting each 128-k stage
+    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, gemm_dma_kernel},  // 2: DMA-fed 128 x 128
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-constexpr int kDmaTile = 6;
+constexpr int kTile64 = 0, kTile64Split = 1, kDmaTile = 2;
 
 }  // namespace
 
@@ -617,7 +613,7 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
   GemmPlan p;
   p.skinny = false;
   p.sk = SkinnyPlan{0, 0, 0};
-  if (K % kTiles[tile].sk != 0) tile = tile == 5 ? 0 : 1;  // stage must divide K
+  if (K % kTiles[tile].sk != 0) tile = kTile64;  // its 64-k stage divides every K here
   p.tile = tile;
   p.block_m = kTiles[tile].bm;
   p.block_n = kTiles[tile].bn;
@@ -640,9 +636,9 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
 // MI355X (graph-replayed, weights read from HBM):
 //   * skinny: every shape up to M = 8; up to M = 16 when K <= 4096 (its per-wave K range grows
 //     with K), and up to M = 32 for small matrices (N*K <= 4.2M: TinyLlama q/o and k/v);
-//   * 64 x 128 with 8 wavefronts (tile 5): M <= 64, and N <= 4096 until the 128 x 128 grid fills
-//     the GPU;
-//   * 64 x 128 with 4 wavefronts (tile 0): wide N (gate/up) at M = 65 .. ~512;
+//   * 64 x 128 with 8 wavefronts (kTile64Split): M <= 64, and N <= 4096 until the 128 x 128 grid
+//     fills the GPU;
+//   * 64 x 128 with 4 wavefronts (kTile64): wide N (gate/up) at M = 65 .. ~512;
 //   * DMA-fed 128 x 128: once it has a tile per CU, or K >= 8192 (long K amortizes its split-K).
 GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
   const int cus = cu_count > 0 ? cu_count : 256;
@@ -656,15 +652,15 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
   }
   int tile;
   if (M <= 64) {
-    tile = k128 ? 5 : 0;
+    tile = k128 ? kTile64Split : kTile64;
   } else {
     const long dma_tiles = (long)ceil_div(M, dma::BM) * ceil_div(N, dma::BN);
     if (dma_tiles >= cus || (K >= 8192 && M > 128))
       tile = kDmaTile;
     else if (N >= 4096 || !k128)
-      tile = 0;
+      tile = kTile64;
     else
-      tile = 5;
+      tile = kTile64Split;
   }
   return gemm_plan_with_tile(M, N, K, cu_count, tile);
 }
