@@ -33,7 +33,8 @@ Protocol
   dwordx4 kernels on 1 GiB buffers; fp16 MFMA peak with torch.matmul
   (hipBLASLt) at 4096/6144/8192.
 * M=2048 (BASELINE config 4's largest point): the MFMA GEMM on every
-  TinyLlama shape; TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum.
+  TinyLlama shape, 10 launches per HIP graph, HIP events around replays;
+  TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum.
 * cpu_baseline: the oracle's FP32 dequant + matmul (numpy; the reference's
   CPU path restated) on the host cores over a bounded sample.
 
@@ -465,8 +466,8 @@ def main() -> int:
         for i, ly in enumerate(layers):
             xm = torch.randn(2048, ly["K"], dtype=torch.float16, device="cuda")
             p, s = dev[0][i]
-            ops.int4_gemm(xm, p, s, GROUP)
-            t = statistics.median(batch_avg_ms(torch, lambda: ops.int4_gemm(xm, p, s, GROUP), 5) for _ in range(5))
+            steps = GraphSteps(torch, lambda r, xm=xm, p=p, s=s: ops.int4_gemm(xm, p, s, GROUP), 10)
+            t = statistics.median(steps.event_avg_ms(10) for _ in range(5))
             fl = 2.0 * 2048 * ly["N"] * ly["K"]
             per[ly["name"]] = {"us": round(t * 1e3, 1), "tflops": round(fl / (t * 1e-3) / 1e12, 1)}
             total_flops += fl

@@ -85,6 +85,14 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
  * which counted floats instead of bytes. */
 size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size);
 
+/* The kernel kf_int4_gemm() runs for (M, N, K, G) on the current device: *kernel is
+ * KF_GEMM_SKINNY or a tile-table index in [0, *num_kernels), *splits the split-K factor
+ * (1 = no workspace), *block_m x *block_n the output tile (0 x 0 for the skinny kernel).
+ * Any output pointer may be NULL.  For diagnostics and tests; no reference counterpart. */
+#define KF_GEMM_SKINNY (-1)
+int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num_kernels,
+                      int* splits, int* block_m, int* block_n);
+
 /* MFMA dequant GEMM, any M >= 1, N % 64 == 0, K % G == 0, G in {64, 128}.
  * ws may be NULL when kf_int4_gemm_workspace_bytes() returned 0.
  * Replaces kf::gemm_tc::run (dequant_gemm_tc_kernel.cuh:203-211) and the

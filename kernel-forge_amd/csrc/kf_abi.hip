@@ -130,6 +130,25 @@ size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size) {
   return kf::gemm_workspace_bytes(kf::gemm_plan(M, N, K, cus), M, N);
 }
 
+int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num_kernels, int* splits, int* block_m,
+                      int* block_n) {
+  if (M < 1 || N < 1 || K < 64 || K % 64)
+    return fail(KF_ERR_INVALID_ARG, "gemm plan needs M, N >= 1 and K a positive multiple of 64, got M=%d N=%d K=%d", M,
+                N, K);
+  if (group_size != 64 && group_size != 128)
+    return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);
+  int cus = 0;
+  const int st = cu_count(&cus);
+  if (st) return st;
+  const kf::GemmPlan p = kf::gemm_plan(M, N, K, cus);
+  if (kernel) *kernel = p.skinny ? KF_GEMM_SKINNY : p.tile;
+  if (num_kernels) *num_kernels = kf::gemm_num_tiles();
+  if (splits) *splits = p.skinny ? 1 : p.splits;
+  if (block_m) *block_m = p.skinny ? 0 : p.block_m;
+  if (block_n) *block_n = p.skinny ? 0 : p.block_n;
+  return KF_OK;
+}
+
 int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y, void* ws, size_t ws_bytes, int M,
                  int N, int K, int group_size, void* stream) {
   int st = check_common(x, packed, scales, y, M, N, K, group_size);
@@ -139,9 +158,9 @@ int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
   int cus = 0;
   if ((st = cu_count(&cus))) return st;
   const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);
-  // One workgroup (<= 512 threads) per output tile, all in grid dimension x.
+  // One workgroup (<= 512 threads) per output tile and split, all in grid dimension x.
   const long long tiles = (long long)((M + plan.block_m - 1) / plan.block_m) * ((N + plan.block_n - 1) / plan.block_n);
-  if (!plan.skinny && (tiles + 8) * 512 > 0x7FFFFFFFLL)
+  if (!plan.skinny && (tiles * plan.splits + 8) * 512 > 0x7FFFFFFFLL)
     return fail(KF_ERR_UNSUPPORTED, "M=%d, N=%d exceed the grid limit for %dx%d tiles", M, N, plan.block_m,
                 plan.block_n);
   const size_t need = kf::gemm_workspace_bytes(plan, M, N);

@@ -25,8 +25,11 @@
 //     16-byte x chunk) and B (one packed word, dequantized with dequant8), so one 8-byte
 //     LDS read gives a lane both sub-steps' weights.
 //   * Tiles are ordered in bands of group_m M-tiles (all N-tiles of a band before the next
-//     band) and the bands are dealt to the 8 XCDs in contiguous runs, so the x rows an XCD
-//     uses stay in its L2 and each weight tile is fetched once per band.
+//     band); the (split, tile) jobs of a launch, split-major, are dealt to the 8 XCDs in
+//     contiguous runs of equal length, so the x rows an XCD uses stay in its L2, each weight
+//     tile is fetched once per band, and no XCD holds more jobs than another (a 1-D grid: the
+//     hardware deals workgroup i to XCD i % 8).
+#include <algorithm>
 #include <type_traits>
 
 #include "kf_device.h"
@@ -36,6 +39,18 @@ namespace kf {
 namespace {
 
 constexpr int kXcds = 8;
+
+// Job of this workgroup in a 1-D grid of ceil(jobs / 8) * 8 workgroups: XCD x (= blockIdx.x % 8)
+// takes jobs x * per_xcd .. + per_xcd - 1.  Job j = split * tiles + tile.  False: no job.
+__device__ __forceinline__ bool gemm_job(int tiles, int splits, int& split, int& tile) {
+  const int jobs = tiles * splits;
+  const int per_xcd = (jobs + kXcds - 1) / kXcds;
+  const int j = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (j >= jobs) return false;
+  split = j / tiles;
+  tile = j - split * tiles;
+  return true;
+}
 
 template <int BM_, int BN_, int WGM_, int WGN_, int WK_, int WAVES_PER_SIMD_ = 2>
 struct TileCfg {
@@ -86,7 +101,7 @@ template <class C>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_SIMD, C::WAVES_PER_SIMD)))
 void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales,
                  half_t* __restrict__ y, float* __restrict__ ws, int M, int N, int K, int log2_group,
-                 int stages_per_split, int tiles_m, int tiles_n, int group_m) {
+                 int stages_per_split, int splits, int tiles_m, int tiles_n, int group_m) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * C::STAGE];
 
   const int tid = threadIdx.x;
@@ -99,11 +114,9 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
   const int g = lane >> 4;
   const int l16 = lane & 15;
 
-  // Tile of this workgroup (see the header comment for the order).
-  const int total = tiles_m * tiles_n;
-  const int per_xcd = (total + kXcds - 1) / kXcds;
-  const int t = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (t >= total) return;
+  // Split and tile of this workgroup (see the header comment for the order).
+  int split, t;
+  if (!gemm_job(tiles_m * tiles_n, splits, split, t)) return;
   const int band = group_m * tiles_n;
   const int bi = t / band;
   const int tb = t - bi * band;
@@ -114,7 +127,7 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
   const int n0 = nt * C::BN;
 
   const int nst = K / C::SK;
-  const int st_begin = blockIdx.y * stages_per_split;
+  const int st_begin = split * stages_per_split;
   const int st_end = min(nst, st_begin + stages_per_split);
   const int ns = st_end - st_begin;
   const int words_per_row = K >> 3;
@@ -297,7 +310,7 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
   }
 
   // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
-  float* part = ws ? ws + (size_t)blockIdx.y * M * N : nullptr;
+  float* part = ws ? ws + (size_t)split * M * N : nullptr;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -374,7 +387,8 @@ __device__ __forceinline__ void dma_u16(uint32_t lds, const void* src) {
 __global__ __launch_bounds__(dma::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
                      const half_t* __restrict__ scales, half_t* __restrict__ y, float* __restrict__ ws, int M, int N,
-                     int K, int log2_group, int stages_per_split, int tiles_m, int tiles_n, int group_m) {
+                     int K, int log2_group, int stages_per_split, int splits, int tiles_m, int tiles_n,
+                     int group_m) {
   using namespace dma;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
 
@@ -386,10 +400,8 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   const int g = lane >> 4;
   const int l16 = lane & 15;
 
-  const int total = tiles_m * tiles_n;
-  const int per_xcd = (total + kXcds - 1) / kXcds;
-  const int t = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (t >= total) return;
+  int split, t;
+  if (!gemm_job(tiles_m * tiles_n, splits, split, t)) return;
   const int band = group_m * tiles_n;
   const int bi = t / band;
   const int tb = t - bi * band;
@@ -398,7 +410,7 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   const int n0 = (tb / gm) * BN;
 
   const int nst = K / BK;
-  const int st_begin = blockIdx.y * stages_per_split;
+  const int st_begin = split * stages_per_split;
   const int last = min(nst, st_begin + stages_per_split) - 1;
   const int ns = last + 1 - st_begin;
 
@@ -536,7 +548,7 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
   if (ws) {
     if (kw == 0) {
-      float* part = ws + (size_t)blockIdx.y * M * N;
+      float* part = ws + (size_t)split * M * N;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -584,41 +596,62 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
 }
 
 typedef void (*GemmFn)(const half_t*, const uint32_t*, const half_t*, half_t*, float*, int, int, int, int, int, int,
-                       int, int);
+                       int, int, int);
 
 struct TileEntry {
   int bm, bn, sk, threads;  // tile, k per stage, workgroup size
+  // Cost terms of the dispatcher (see gemm_plan): workgroups resident per CU, and the time of
+  // one round of resident workgroups, us_per_gmac * 1e-9 * BM * BN * k + us_fixed microseconds
+  // for k = the split's k range.  0 blocks_per_cu: never chosen by the cost model.
+  int blocks_per_cu;
+  double us_per_gmac, us_fixed;
   GemmFn fn;
 };
 
 template <class C>
-TileEntry entry() {
-  return TileEntry{C::BM, C::BN, C::SK, C::THREADS, gemm_kernel<C>};
+TileEntry entry(int blocks_per_cu, double us_per_gmac, double us_fixed) {
+  return TileEntry{C::BM, C::BN, C::SK, C::THREADS, blocks_per_cu, us_per_gmac, us_fixed, gemm_kernel<C>};
 }
 
-// Tile table: index = GemmPlan::tile.
+// Tile table: index = GemmPlan::tile.  Cost terms: least-squares fit (log-time) of the model
+// in gemm_plan to graph-replayed timings of every tile and split count over the TinyLlama and
+// Qwen2.5 layer shapes, M = 16 .. 4096, on MI355X (3,460 points, rms error 7.0%).
 const TileEntry kTiles[] = {
-    entry<TileCfg<64, 128, 1, 4, 1>>(),  // 0: 64 x 128, 4 wavefronts (wave 64 x 32)
-    entry<TileCfg<64, 128, 1, 4, 2>>(),  // 1: 64 x 128, 8 wavefronts splitting each 128-k stage
-    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, gemm_dma_kernel},  // 2: DMA-fed 128 x 128
+    entry<TileCfg<64, 128, 1, 4, 1>>(0, 0.0, 0.0),         // 0: 64 x 128, 4 waves; 64-k stages (any K)
+    entry<TileCfg<64, 128, 1, 4, 2>>(1, 625.47, 3.039),    // 1: 64 x 128, 8 waves (2 k-groups)
+    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, 2, 538.68, 5.589, gemm_dma_kernel},  // 2: DMA 128 x 128
+    entry<TileCfg<32, 128, 1, 4, 2>>(1, 906.11, 2.112),    // 3: 32 x 128, 8 waves (2 k-groups)
+    entry<TileCfg<32, 64, 1, 2, 4>>(1, 1032.15, 2.504),    // 4: 32 x 64, 8 waves (4 k-groups, 256-k stages)
+    entry<TileCfg<16, 64, 1, 2, 4>>(1, 1761.05, 1.935),    // 5: 16 x 64, 8 waves (4 k-groups, 256-k stages)
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-constexpr int kTile64 = 0, kTile64Split = 1, kDmaTile = 2;
+constexpr int kTile64 = 0, kDmaTile = 2;
+// Split-K costs one more launch plus the fp32 partials: kSplitUs + kSplitUsPerElem * splits * M * N
+// (same fit), and is taken only when the model predicts it at least 10% faster.
+constexpr double kSplitUs = 2.786, kSplitUsPerElem = 1.5147e-6, kSplitMargin = 0.9;
+constexpr int kMaxSplits = 12;  // the largest split count the fit was measured on
+
+GemmPlan plan_for(int K, int tile, int splits) {
+  GemmPlan p;
+  p.skinny = false;
+  p.sk = SkinnyPlan{0, 0, 0};
+  p.tile = tile;
+  p.block_m = kTiles[tile].bm;
+  p.block_n = kTiles[tile].bn;
+  const int nst = K / kTiles[tile].sk;
+  p.kt_per_split = ceil_div(nst, splits);
+  p.splits = ceil_div(nst, p.kt_per_split);  // no empty splits
+  return p;
+}
 
 }  // namespace
 
 int gemm_num_tiles() { return kNumTiles; }
 
 GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
-  GemmPlan p;
-  p.skinny = false;
-  p.sk = SkinnyPlan{0, 0, 0};
   if (K % kTiles[tile].sk != 0) tile = kTile64;  // its 64-k stage divides every K here
-  p.tile = tile;
-  p.block_m = kTiles[tile].bm;
-  p.block_n = kTiles[tile].bn;
   const int nst = K / kTiles[tile].sk;
-  const long tiles = (long)ceil_div(N, p.block_n) * ceil_div(M, p.block_m);
+  const long tiles = (long)ceil_div(N, kTiles[tile].bn) * ceil_div(M, kTiles[tile].bm);
   const long want = cu_count > 0 ? cu_count : 256;
   int splits = 1;
   if (tiles < want) {
@@ -627,42 +660,61 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
   }
-  p.kt_per_split = ceil_div(nst, splits);
-  p.splits = ceil_div(nst, p.kt_per_split);  // no empty splits
-  return p;
+  return plan_for(K, tile, splits);
 }
 
-// Kernel choice, from a sweep of every TinyLlama / Qwen2.5 layer shape over M = 16 .. 2048 on
-// MI355X (graph-replayed, weights read from HBM):
-//   * skinny: every shape up to M = 8; up to M = 16 when K <= 4096 (its per-wave K range grows
-//     with K), and up to M = 32 for small matrices (N*K <= 4.2M: TinyLlama q/o and k/v);
-//   * 64 x 128 with 8 wavefronts (kTile64Split): M <= 64, and N <= 4096 until the 128 x 128 grid
-//     fills the GPU;
-//   * 64 x 128 with 4 wavefronts (kTile64): wide N (gate/up) at M = 65 .. ~512;
-//   * DMA-fed 128 x 128: once it has a tile per CU, or K >= 8192 (long K amortizes its split-K).
+// Kernel choice.
+//   * The skinny kernel (one weight stream, K split inside the workgroup) for M <= 8, for
+//     M <= 16 when K <= 4096, and up to M = 32 for small matrices (N*K <= 4.2M: TinyLlama q/o
+//     and k/v).  The rule depends on N only through that last clause, so concatenated q|k|v or
+//     gate|up rows take the same kernel as the separate layers for M <= 16 (bit-identical
+//     columns).
+//   * Otherwise the tile and split-K factor that minimise a fitted cost: each XCD runs its
+//     share of the tiles x splits workgroups in rounds of blocks_per_cu * cu_count / 8; a round
+//     costs the tile entry's us_per_gmac * 1e-9 * BM * BN * (K / splits) + us_fixed, and
+//     splitting adds its own cost (see kSplitUs).  Measured effect: small tiles (16 x 64,
+//     32 x 64) at medium M and for narrow N (k/v projections), the DMA tile once it fills the
+//     GPU, split-K only for long K.
 GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
   const int cus = cu_count > 0 ? cu_count : 256;
   const bool k128 = K % 128 == 0;
   if (M <= kSkinnyMaxM && k128 && (M <= 8 || (K <= 4096 && (M <= 16 || (long)N * K <= 4200000L)))) {
-    GemmPlan p = gemm_plan_with_tile(M, N, K, cu_count, 0);
+    GemmPlan p = plan_for(K, kTile64, 1);
     p.skinny = true;
-    p.splits = 1;
     p.sk = skinny_plan(M, N, K, cu_count);
     return p;
   }
-  int tile;
-  if (M <= 64) {
-    tile = k128 ? kTile64Split : kTile64;
-  } else {
+  if (!k128) {  // K % 64 == 0 only: the 64-k-stage kernels
     const long dma_tiles = (long)ceil_div(M, dma::BM) * ceil_div(N, dma::BN);
-    if (dma_tiles >= cus || (K >= 8192 && M > 128))
-      tile = kDmaTile;
-    else if (N >= 4096 || !k128)
-      tile = kTile64;
-    else
-      tile = kTile64Split;
+    return gemm_plan_with_tile(M, N, K, cu_count, dma_tiles >= cus ? kDmaTile : kTile64);
   }
-  return gemm_plan_with_tile(M, N, K, cu_count, tile);
+  int best_tile = kDmaTile, best_splits = 1;
+  double best = 1e300;
+  for (int tile = 0; tile < kNumTiles; ++tile) {
+    const TileEntry& e = kTiles[tile];
+    if (e.blocks_per_cu == 0 || K % e.sk != 0) continue;
+    const int nst = K / e.sk;
+    const long tiles = (long)ceil_div(M, e.bm) * ceil_div(N, e.bn);
+    const int max_splits = std::min(kMaxSplits, std::max(1, nst / 4));  // >= 4 stages per split
+    int prev = 0;
+    for (int s = 1; s <= max_splits; ++s) {
+      const int splits = ceil_div(nst, ceil_div(nst, s));
+      if (splits == prev) continue;
+      prev = splits;
+      // Jobs are dealt evenly to the XCDs (gemm_job); each XCD runs its share in rounds.
+      const long per_xcd = (tiles * splits + kXcds - 1) / kXcds;
+      const long slots = std::max(1L, (long)e.blocks_per_cu * cus / kXcds);
+      const long rounds = (per_xcd + slots - 1) / slots;
+      double cost = rounds * (e.us_per_gmac * 1e-9 * e.bm * e.bn * ((double)K / splits) + e.us_fixed);
+      if (splits > 1) cost = (cost + kSplitUs + kSplitUsPerElem * splits * (double)M * N) / kSplitMargin;
+      if (cost < best) {
+        best = cost;
+        best_tile = tile;
+        best_splits = splits;
+      }
+    }
+  }
+  return plan_for(K, best_tile, best_splits);
 }
 
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
@@ -676,15 +728,15 @@ hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, con
   const int log2_group = group_size == 128 ? 7 : 6;
   const int tiles_m = ceil_div(M, e.bm);
   const int tiles_n = ceil_div(N, e.bn);
-  const int total = tiles_m * tiles_n;
-  const int grid_x = ceil_div(total, kXcds) * kXcds;
+  const int grid_x = ceil_div(tiles_m * tiles_n * p.splits, kXcds) * kXcds;
   // Bands of M-tiles: one band per XCD when the M-tiles divide evenly, else single rows.
   int group_m = tiles_m / kXcds;
   if (group_m < 1) group_m = 1;
   float* part = p.splits > 1 ? static_cast<float*>(ws) : nullptr;
-  hipLaunchKernelGGL(e.fn, dim3(grid_x, p.splits), dim3(e.threads), 0, stream, static_cast<const half_t*>(x),
+  hipLaunchKernelGGL(e.fn, dim3(grid_x), dim3(e.threads), 0, stream, static_cast<const half_t*>(x),
                      static_cast<const uint32_t*>(packed), static_cast<const half_t*>(scales),
-                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split, tiles_m, tiles_n, group_m);
+                     static_cast<half_t*>(y), part, M, N, K, log2_group, p.kt_per_split, p.splits, tiles_m, tiles_n,
+                     group_m);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const size_t mn = (size_t)M * N;

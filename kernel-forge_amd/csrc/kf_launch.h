@@ -65,7 +65,7 @@ struct GemmPlan {
   int block_m;     // BM
   int block_n;     // BN
   int splits;      // split-K factor (1 = no workspace)
-  int kt_per_split;// k-tiles of 64 per split
+  int kt_per_split;// k stages (of the tile's stage depth) per split
 };
 GemmPlan gemm_plan(int M, int N, int K, int cu_count);
 // Plan with an explicit tile-table entry (used by the measured dispatcher table and tuning).

@@ -70,9 +70,12 @@ def sweep(ms: list[int], shapes: dict, group: int = 128) -> dict:
                 row["gemv_us"] = time_us(lambda c: ops.int4_gemv(x, dev[c][0], dev[c][1], group), copies)
             if n % 64 == 0:
                 row["gemm_us"] = time_us(lambda c: ops.int4_gemm(x, dev[c][0], dev[c][1], group), copies)
-            row["tflops_best"] = 2 * m * n * k / min(row.values()) / 1e6
+                plan = ops.gemm_plan(m, n, k, group)
+                row["gemm_kernel"] = f"{plan['kernel']}/{plan['splits']}"  # tile-table index (or skinny) / splits
+            row["tflops_best"] = 2 * m * n * k / min(v for kk, v in row.items() if kk.endswith("_us")) / 1e6
             res[name][m] = row
-            print(f"{name} M={m}: " + " ".join(f"{kk}={v:.2f}" for kk, v in row.items()), flush=True)
+            print(f"{name} M={m}: " + " ".join(f"{kk}={v:.2f}" if isinstance(v, float) else f"{kk}={v}"
+                                              for kk, v in row.items()), flush=True)
         del dev
         torch.cuda.empty_cache()
     return res

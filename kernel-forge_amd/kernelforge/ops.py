@@ -13,6 +13,8 @@ Inference only: no backward formulas are registered.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from kernelforge import _lib
@@ -118,6 +120,21 @@ def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group
                                   _stream_ptr(x.device))
     _lib.check(status, "int4_gemm")
     return y
+
+
+def gemm_plan(m: int, n: int, k: int, group_size: int = 128, device: torch.device | None = None) -> dict:
+    """The kernel int4_gemm runs for an [m, k] x [n, k]^T problem on `device` (default: current).
+
+    Returns {"kernel": "skinny" or the tile-table index, "num_kernels": table size,
+    "splits": split-K factor, "tile": (BM, BN)}.  Diagnostics; no reference counterpart.
+    """
+    lib = _lib.load()
+    out = [ctypes.c_int() for _ in range(5)]
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        status = lib.kf_int4_gemm_plan(int(m), int(n), int(k), int(group_size), *[ctypes.byref(v) for v in out])
+    _lib.check(status, "gemm_plan")
+    kernel, num, splits, bm, bn = (v.value for v in out)
+    return {"kernel": "skinny" if kernel < 0 else kernel, "num_kernels": num, "splits": splits, "tile": (bm, bn)}
 
 
 def int4_matmul(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:

@@ -220,7 +220,8 @@ def test_gemm_rejects_n_not_multiple_of_64():
         ops.int4_gemm(x, dp, ds, 128)
 
 
-@pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, True), ("tinyllama_down", 64, True),
+@pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, False), ("tinyllama_down", 64, True),
+                                             ("qwen_down", 32, True), ("tinyllama_down", 2048, True),
                                              ("tinyllama_gate_up", 16, False), ("tinyllama_gate_up", 768, False)])
 def test_gemm_is_deterministic(layer, m, splitk):
     """Split-K partials, the DMA kernel's in-block k-group halves and the skinny kernel's
@@ -232,6 +233,25 @@ def test_gemm_is_deterministic(layer, m, splitk):
     assert (ws > 0) == splitk, f"expected {'a' if splitk else 'no'} split-K workspace at M={m}"
     outs = [ops.int4_gemm(x, dp, ds, 128) for _ in range(3)]
     assert all(torch.equal(outs[0], o_) for o_ in outs[1:])
+
+
+def test_dispatcher_covers_every_gemm_kernel():
+    """The GEMM shapes of this file reach every kernel of the tile table, the skinny kernel, and
+    split-K on both a register-staged tile and the DMA tile, so each is checked above."""
+    cases = [(m, *LAYER_SHAPES[layer]) for layer in LAYER_SHAPES for m in (1, 8, 9, 16, 17, 32, 64, 65, 128)]
+    cases += [(m, *LAYER_SHAPES[layer]) for layer in ("tinyllama_gate_up", "tinyllama_down")
+              for m in (200, 256, 512, 2048)]
+    cases += [(33, 128, 4160), (65, 192, 512), (17, 5632, 2048), (300, 2048, 5632)]
+    plans = [ops.gemm_plan(m, n, k, 128) for m, n, k in cases]
+    kernels = {p["kernel"] for p in plans}
+    num = plans[0]["num_kernels"]
+    assert kernels == {"skinny", *range(num)}, f"kernels reached: {sorted(map(str, kernels))} of {num} + skinny"
+    split_kernels = {p["kernel"] for p in plans if p["splits"] > 1}
+    assert any(p["tile"] == (128, 128) and p["splits"] > 1 for p in plans), "no DMA split-K case"
+    assert any(p["tile"] != (128, 128) and p["splits"] > 1 for p in plans), f"split-K only on {split_kernels}"
+    for (m, n, k), p in zip(cases, plans):
+        ws = _lib.load().kf_int4_gemm_workspace_bytes(m, n, k, 128)
+        assert (ws > 0) == (p["splits"] > 1)
 
 
 # ---------------------------------------------------------------------------
@@ -371,10 +391,12 @@ def test_quantize_linears_swaps_decoder_linears():
         blk.q_proj(torch.randn(1, 256, device=DEV))
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 128])
-def test_hip_graph_capture_replays_match_eager(m):
-    """Capture int4_linear (GEMV or GEMM + split-K) in a graph; every replay equals eager bitwise."""
-    n, k = LAYER_SHAPES["tinyllama_gate_up"]
+@pytest.mark.parametrize("layer,m", [("tinyllama_gate_up", 1), ("tinyllama_gate_up", 4), ("tinyllama_gate_up", 16),
+                                     ("tinyllama_gate_up", 128), ("tinyllama_down", 64)])
+def test_hip_graph_capture_replays_match_eager(layer, m):
+    """Capture int4_linear (GEMV, skinny, tiled GEMM, GEMM + split-K) in a graph; every replay
+    equals eager bitwise."""
+    n, k = LAYER_SHAPES[layer]
     _, _, dp, ds = _weights(n, k, 128)
     static_x = torch.from_numpy(_x(m, k, 23)).to(DEV)
     eager = ops.int4_linear(static_x, dp, ds, 128)
