@@ -6,9 +6,15 @@
 // 32-k chunk (32 divides G), so W_hat is never rounded to fp16 here.
 //
 // One launch serves up to kMaxGemvGroup independent problems (x_p, W_p, y_p,
-// N_p, K_p) with a common M and G; a plain GEMV is a group of one.  On MI355X
-// an empty launch already costs ~1.6 us, longer than streaming a 2 MB layer,
-// so independent decode linears should share a launch.
+// N_p, K_p) with a common M and G (gemv_grouped_kernel), or one problem
+// (gemv_kernel).  On MI355X an empty launch already costs ~1.6 us, longer than
+// streaming a 2 MB layer, so independent decode linears should share a launch.
+// A wavefront lives for one or a few memory round trips, so whatever it must
+// read before its first weight load is on the critical path: the single-problem
+// kernel takes every argument as a preloaded scalar, and the grouped kernel
+// finds its problem from a preloaded header and then reads that problem's
+// descriptor in one round of scalar loads (a problem lookup through two
+// dependent scalar loads cost 0.3-0.5 us per launch).
 //
 // Mapping (bandwidth-first, no LDS, no MFMA):
 //   * A "chunk" is 32 consecutive k of one row: 16 B of packed words (one
@@ -32,6 +38,7 @@
 //     fp16 (RNE) and stores them.  Rows past N_p are clamped to row N_p - 1
 //     for loading and never stored.
 #include <limits.h>
+#include <stddef.h>
 
 #include "kf_device.h"
 #include "kf_launch.h"
@@ -150,44 +157,23 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
   }
 }
 
+// Rows row0 .. row0 + R - 1 of one problem (the body both entry kernels share, so a problem
+// gives the same bits whichever kernel runs it).
 template <int M, int R, int UMAX>
-__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const GemvBatch batch) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gwave = blockIdx.x * kGemvWavesPerBlock + wave;
-
-  // Problem lookup (uniform per wave) from the header alone: it is the first
-  // 64 bytes of the kernel arguments, read in one scalar load (or preloaded
-  // into SGPRs where the firmware supports kernarg preloading).
-  typedef int hdr_t __attribute__((ext_vector_type(kGemvHdr)));
-  const hdr_t h = *reinterpret_cast<const hdr_t*>(batch.hdr);
-  const int count = h[0];
-  int p = 0, base = 0;
-#pragma unroll
-  for (int i = 1; i <= kMaxGemvGroup; ++i) {
-    const int wb = h[2 + i];
-    if (gwave >= wb) {
-      p = i;
-      base = wb;
-    }
-  }
-  if (p >= count) return;  // past the last problem's waves
-
-  const GemvProblem& pr = batch.prob[p];
+__device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packed, const half_t* scales,
+                                          half_t* y, int N, int K, int scale_shift, int row0, int lane) {
   RowSet<R> rs;
-  rs.x = static_cast<const half_t*>(pr.x);
-  rs.K = pr.K;
-  rs.chunks = pr.K >> 5;
-  rs.scale_shift = h[1];
-  const int N = pr.N;
-  const int row0 = (gwave - base) * R;
-  const int words = pr.K >> 3;
-  const int groups = rs.chunks >> rs.scale_shift;
+  rs.x = x;
+  rs.K = K;
+  rs.chunks = K >> 5;
+  rs.scale_shift = scale_shift;
+  const int words = K >> 3;
+  const int groups = rs.chunks >> scale_shift;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int n = min(row0 + r, N - 1);
-    rs.prow[r] = static_cast<const uint32_t*>(pr.packed) + (size_t)n * words;
-    rs.srow[r] = static_cast<const half_t*>(pr.scales) + (size_t)n * groups;
+    rs.prow[r] = packed + (size_t)n * words;
+    rs.srow[r] = scales + (size_t)n * groups;
   }
 
   float acc[M][R];
@@ -219,7 +205,6 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const Gem
     for (int r = 0; r < R; ++r) acc[m][r] = wave_sum_lane63(acc[m][r]);
 
   if (lane == 63) {
-    half_t* y = static_cast<half_t*>(pr.y);
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -228,33 +213,91 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const Gem
   }
 }
 
-typedef void (*GemvFn)(const GemvBatch);
+// One problem: every argument is a scalar kernel argument, preloaded into SGPRs, so a
+// wavefront issues its weight loads without waiting on any scalar memory access.
+template <int M, int R, int UMAX>
+__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const half_t* __restrict__ x,
+                                                                     const uint32_t* __restrict__ packed,
+                                                                     const half_t* __restrict__ scales,
+                                                                     half_t* __restrict__ y, int N, int K,
+                                                                     int scale_shift) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  if (row0 >= N) return;  // past the last row
+  gemv_rows<M, R, UMAX>(x, packed, scales, y, N, K, scale_shift, row0, lane);
+}
 
-template <int M, int R>
-GemvFn pick_u(int U) {
+// Several problems.  b1 .. b8: first global wavefront of problems 1 .. 8 (ascending; the
+// total after the last problem, then INT_MAX), so one comparison chain on preloaded SGPRs
+// finds both the problem and whether the wave has work.  The problem's descriptor is then
+// read in one round of scalar loads (pointers and sizes together); the pointers are global
+// memory, which the casts state so the loads stay global_load rather than flat_load.
+template <int M, int R, int UMAX>
+__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(int count, int scale_shift, int b1,
+                                                                             int b2, int b3, int b4, int b5, int b6,
+                                                                             int b7, int b8,
+                                                                             const GemvTable table) {
+  const int lane = threadIdx.x & 63;
+  const int gwave = blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bounds[kMaxGemvGroup] = {b1, b2, b3, b4, b5, b6, b7, b8};
+  int p = 0, base = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxGemvGroup; ++i) {
+    if (gwave >= bounds[i]) {
+      p = i + 1;
+      base = bounds[i];
+    }
+  }
+  if (p >= count) return;  // past the last problem's waves
+
+  typedef unsigned long long u64x4 __attribute__((ext_vector_type(4)));
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  static_assert(sizeof(GemvProblem) == 40 && offsetof(GemvProblem, N) == 32, "descriptor layout");
+  const char* desc = reinterpret_cast<const char*>(&table.prob[p]);
+  const u64x4 ptr = *reinterpret_cast<const u64x4*>(desc);  // x, packed, scales, y
+  const i32x2 nk = *reinterpret_cast<const i32x2*>(desc + 32);
+  typedef const __attribute__((address_space(1))) half_t* gh_t;
+  typedef const __attribute__((address_space(1))) uint32_t* gu_t;
+  typedef __attribute__((address_space(1))) half_t* gy_t;
+  gemv_rows<M, R, UMAX>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
+                        (half_t*)(gy_t)ptr.w, nk.x, nk.y, scale_shift, (gwave - base) * R, lane);
+}
+
+typedef void (*GemvFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int);
+typedef void (*GemvGroupedFn)(int, int, int, int, int, int, int, int, int, int, const GemvTable);
+
+template <int M, int R, int U>
+struct GemvKernels {
+  static constexpr GemvFn single = gemv_kernel<M, R, U>;
+  static constexpr GemvGroupedFn grouped = gemv_grouped_kernel<M, R, U>;
+};
+
+template <bool GROUPED, int M, int R>
+auto pick_u(int U) {
   switch (U) {
-    case 1: return gemv_kernel<M, R, 1>;
-    case 2: return gemv_kernel<M, R, 2>;
-    case 3: return gemv_kernel<M, R, 3>;
-    default: return gemv_kernel<M, R, 4>;
+    case 1: return GROUPED ? (void*)GemvKernels<M, R, 1>::grouped : (void*)GemvKernels<M, R, 1>::single;
+    case 2: return GROUPED ? (void*)GemvKernels<M, R, 2>::grouped : (void*)GemvKernels<M, R, 2>::single;
+    case 3: return GROUPED ? (void*)GemvKernels<M, R, 3>::grouped : (void*)GemvKernels<M, R, 3>::single;
+    default: return GROUPED ? (void*)GemvKernels<M, R, 4>::grouped : (void*)GemvKernels<M, R, 4>::single;
   }
 }
 
-template <int M>
-GemvFn pick_r(int R, int U) {
-  return R == 1 ? pick_u<M, 1>(U) : pick_u<M, 2>(U);
+template <bool GROUPED, int M>
+void* pick_r(int R, int U) {
+  return R == 1 ? pick_u<GROUPED, M, 1>(U) : pick_u<GROUPED, M, 2>(U);
 }
 
-GemvFn pick(int M, int R, int U) {
+template <bool GROUPED>
+void* pick(int M, int R, int U) {
   switch (M) {
-    case 1: return pick_r<1>(R, U);
-    case 2: return pick_r<2>(R, U);
-    case 3: return pick_r<3>(R, U);
-    case 4: return pick_r<4>(R, U);
-    case 5: return pick_r<5>(R, U);
-    case 6: return pick_r<6>(R, U);
-    case 7: return pick_r<7>(R, U);
-    default: return pick_r<8>(R, U);
+    case 1: return pick_r<GROUPED, 1>(R, U);
+    case 2: return pick_r<GROUPED, 2>(R, U);
+    case 3: return pick_r<GROUPED, 3>(R, U);
+    case 4: return pick_r<GROUPED, 4>(R, U);
+    case 5: return pick_r<GROUPED, 5>(R, U);
+    case 6: return pick_r<GROUPED, 6>(R, U);
+    case 7: return pick_r<GROUPED, 7>(R, U);
+    default: return pick_r<GROUPED, 8>(R, U);
   }
 }
 
@@ -286,6 +329,16 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
 
 hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int count, int M, int group_size,
                        hipStream_t stream) {
+  const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
+  if (count == 1) {
+    const GemvProblem& q = problems[0];
+    const int blocks = ceil_div(ceil_div(q.N, plan.rows_per_wave), kGemvWavesPerBlock);
+    hipLaunchKernelGGL(reinterpret_cast<GemvFn>(pick<false>(M, plan.rows_per_wave, plan.unroll)), dim3(blocks),
+                       dim3(64 * kGemvWavesPerBlock), 0, stream, static_cast<const half_t*>(q.x),
+                       static_cast<const uint32_t*>(q.packed), static_cast<const half_t*>(q.scales),
+                       static_cast<half_t*>(q.y), q.N, q.K, shift);
+    return hipGetLastError();
+  }
   // Longest rows first: their waves carry the most bytes, so they are
   // dispatched before the short ones (outputs do not depend on the order).
   int order[kMaxGemvGroup];
@@ -296,20 +349,22 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
       order[j] = order[j - 1];
       order[j - 1] = t;
     }
-  GemvBatch batch = {};
-  batch.hdr[0] = count;
-  batch.hdr[1] = group_size == 128 ? 2 : 1;  // log2(G / 32)
+  GemvTable table = {};
+  int bounds[kMaxGemvGroup];  // first wave of problems 1 .., then the total, then INT_MAX
   int waves = 0;
-  for (int i = 0; i < count; ++i) {
-    batch.prob[i] = problems[order[i]];
-    batch.hdr[2 + i] = waves;
-    waves += ceil_div(problems[order[i]].N, plan.rows_per_wave);
+  for (int i = 0; i < kMaxGemvGroup; ++i) {
+    if (i < count) {
+      table.prob[i] = problems[order[i]];
+      waves += ceil_div(problems[order[i]].N, plan.rows_per_wave);
+      bounds[i] = waves;
+    } else {
+      bounds[i] = INT_MAX;
+    }
   }
-  batch.hdr[2 + count] = waves;
-  for (int i = 3 + count; i < kGemvHdr; ++i) batch.hdr[i] = INT_MAX;
   const int blocks = ceil_div(waves, kGemvWavesPerBlock);
-  hipLaunchKernelGGL(pick(M, plan.rows_per_wave, plan.unroll), dim3(blocks), dim3(64 * kGemvWavesPerBlock), 0,
-                     stream, batch);
+  hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(pick<true>(M, plan.rows_per_wave, plan.unroll)), dim3(blocks),
+                     dim3(64 * kGemvWavesPerBlock), 0, stream, count, shift, bounds[0], bounds[1], bounds[2], bounds[3],
+                     bounds[4], bounds[5], bounds[6], bounds[7], table);
   return hipGetLastError();
 }
 

@@ -22,16 +22,11 @@ struct GemvProblem {
   int K;
 };
 
-// Passed by value as the kernel argument (no device-side descriptor buffer).
-// hdr is read by each wavefront with a single 64-byte scalar load:
-//   hdr[0] = count, hdr[1] = log2(G / 32) (32-k chunks per scale group),
-//   hdr[2 + i] = first global wavefront of problem i (ascending), with
-//   hdr[2 + count] = total wavefronts and INT_MAX after it, so one comparison
-//   chain finds both the problem and whether the wave has any work.
-constexpr int kGemvHdr = 16;
-static_assert(kMaxGemvGroup + 4 <= kGemvHdr, "header too small for the group limit");
-struct GemvBatch {
-  int hdr[kGemvHdr];
+// The grouped kernel's arguments: the lookup header as ten scalar arguments (preloaded into
+// SGPRs at wave launch), then this table by value.  A wavefront finds its problem from the
+// header without memory traffic and then fetches that problem's 40-byte descriptor in one
+// round of scalar loads (see kf_gemv.hip).
+struct GemvTable {
   GemvProblem prob[kMaxGemvGroup];
 };
 
