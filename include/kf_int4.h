@@ -101,6 +101,27 @@ int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num
 int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
                  void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream);
 
+/* MFMA-16 block copy of a packed weight (an internal layout; the public packed format is
+ * unchanged): for every 16 rows of W and 128-k super-step, the 64 lanes' 16-byte pieces of
+ * the MFMA fragments stored contiguously in lane order (lane l: row 16b + l%16, words
+ * 16s + 4(l/16) .. +3), rows padded to a multiple of 16 by repeating row N-1; scales as
+ * [ceil(N/16)][K/G][16].  K must be a multiple of 128.  Sizes of the two buffers: */
+int kf_int4_mfma16_sizes(int N, int K, int group_size, size_t* packed_bytes, size_t* scales_bytes);
+
+/* Writes the MFMA-16 copy of (packed, scales) into (packed_r, scales_r); a pure permutation.
+ * The weight copy behind the op that the reference names as its next GEMM step
+ * (docs/phase4-notes.md:59, docs/references.md:26); no reference function. */
+int kf_int4_reorder_mfma16(const void* packed, const void* scales, void* packed_r, void* scales_r,
+                           int N, int K, int group_size, void* stream);
+
+/* kf_int4_gemm with the MFMA-16 copy of the same weight: where the skinny kernel runs it
+ * streams packed_r / scales_r (contiguous 1 KiB wavefront loads, 7-15% faster), elsewhere
+ * packed / scales.  Results are bit-identical to kf_int4_gemm.  Same requirements, plus
+ * K % 128 == 0.  No reference counterpart (see kf_int4_reorder_mfma16). */
+int kf_int4_gemm_mfma16(const void* x, const void* packed, const void* scales, const void* packed_r,
+                        const void* scales_r, void* y, void* ws, size_t ws_bytes,
+                        int M, int N, int K, int group_size, void* stream);
+
 /* W_hat = fp16_rne(q * s) as fp16 [N, K]: the dequantization the GEMM feeds
  * to the matrix cores, exported so it can be compared bit for bit with the
  * reference's dequantize(qw, torch.float16) (kernelforge/quantize.py:108-113). */

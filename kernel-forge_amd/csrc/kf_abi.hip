@@ -76,6 +76,33 @@ int check_common(const void* x, const void* packed, const void* scales, const vo
   return KF_OK;
 }
 
+// kf_int4_gemm and kf_int4_gemm_mfma16: validation, plan, workspace check, launch.
+int gemm_entry(const void* x, const void* packed, const void* scales, const void* packed_r, const void* scales_r,
+               void* y, void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream) {
+
+  int st = check_common(x, packed, scales, y, M, N, K, group_size);
+  if (st) return st;
+  if (N % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs N to be a multiple of 64, got N=%d", N);
+  if (K % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs K to be a multiple of 64, got K=%d", K);
+  int cus = 0;
+  if ((st = cu_count(&cus))) return st;
+  const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);
+  // One workgroup (<= 512 threads) per output tile and split, all in grid dimension x.
+  const long long tiles = (long long)((M + plan.block_m - 1) / plan.block_m) * ((N + plan.block_n - 1) / plan.block_n);
+  if (!plan.skinny && (tiles * plan.splits + 8) * 512 > 0x7FFFFFFFLL)
+    return fail(KF_ERR_UNSUPPORTED, "M=%d, N=%d exceed the grid limit for %dx%d tiles", M, N, plan.block_m,
+                plan.block_n);
+  const size_t need = kf::gemm_workspace_bytes(plan, M, N);
+  if (need > 0) {
+    if (!ws) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got NULL", need);
+    if (ws_bytes < need) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got %zu", need, ws_bytes);
+    if (!aligned(ws, 16)) return fail(KF_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
+  }
+  return hip_status(kf::gemm_launch(plan, x, packed, scales, y, ws, M, N, K, group_size,
+                                    static_cast<hipStream_t>(stream), packed_r, scales_r),
+                    "int4_gemm launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -151,27 +178,39 @@ int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num
 
 int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y, void* ws, size_t ws_bytes, int M,
                  int N, int K, int group_size, void* stream) {
-  int st = check_common(x, packed, scales, y, M, N, K, group_size);
+  return gemm_entry(x, packed, scales, nullptr, nullptr, y, ws, ws_bytes, M, N, K, group_size, stream);
+}
+
+int kf_int4_mfma16_sizes(int N, int K, int group_size, size_t* packed_bytes, size_t* scales_bytes) {
+  if (N < 1 || K < 128 || K % 128 || (group_size != 64 && group_size != 128))
+    return fail(KF_ERR_INVALID_ARG, "MFMA-16 layout needs N >= 1, K a multiple of 128 and G in (64, 128), got N=%d K=%d G=%d",
+                N, K, group_size);
+  if (packed_bytes) *packed_bytes = kf::mfma16_packed_words(N, K) * 4;
+  if (scales_bytes) *scales_bytes = kf::mfma16_scale_count(N, K, group_size) * 2;
+  return KF_OK;
+}
+
+int kf_int4_reorder_mfma16(const void* packed, const void* scales, void* packed_r, void* scales_r, int N, int K,
+                           int group_size, void* stream) {
+  if (!packed || !scales || !packed_r || !scales_r)
+    return fail(KF_ERR_INVALID_ARG, "packed, scales, packed_r and scales_r must be non-null");
+  int st = kf_int4_mfma16_sizes(N, K, group_size, nullptr, nullptr);
   if (st) return st;
-  if (N % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs N to be a multiple of 64, got N=%d", N);
-  if (K % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs K to be a multiple of 64, got K=%d", K);
-  int cus = 0;
-  if ((st = cu_count(&cus))) return st;
-  const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);
-  // One workgroup (<= 512 threads) per output tile and split, all in grid dimension x.
-  const long long tiles = (long long)((M + plan.block_m - 1) / plan.block_m) * ((N + plan.block_n - 1) / plan.block_n);
-  if (!plan.skinny && (tiles * plan.splits + 8) * 512 > 0x7FFFFFFFLL)
-    return fail(KF_ERR_UNSUPPORTED, "M=%d, N=%d exceed the grid limit for %dx%d tiles", M, N, plan.block_m,
-                plan.block_n);
-  const size_t need = kf::gemm_workspace_bytes(plan, M, N);
-  if (need > 0) {
-    if (!ws) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got NULL", need);
-    if (ws_bytes < need) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got %zu", need, ws_bytes);
-    if (!aligned(ws, 16)) return fail(KF_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
-  }
-  return hip_status(kf::gemm_launch(plan, x, packed, scales, y, ws, M, N, K, group_size,
-                                    static_cast<hipStream_t>(stream)),
-                    "int4_gemm launch");
+  if (!aligned(packed, 16) || !aligned(packed_r, 16)) return fail(KF_ERR_INVALID_ARG, "packed and packed_r must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(scales_r, 2)) return fail(KF_ERR_INVALID_ARG, "scales and scales_r must be 2-byte aligned");
+  return hip_status(kf::reorder_mfma16_launch(packed, scales, packed_r, scales_r, N, K, group_size,
+                                              static_cast<hipStream_t>(stream)),
+                    "reorder_mfma16 launch");
+}
+
+int kf_int4_gemm_mfma16(const void* x, const void* packed, const void* scales, const void* packed_r,
+                        const void* scales_r, void* y, void* ws, size_t ws_bytes, int M, int N, int K, int group_size,
+                        void* stream) {
+  if (!packed_r || !scales_r) return fail(KF_ERR_INVALID_ARG, "packed_r and scales_r must be non-null");
+  int st = kf_int4_mfma16_sizes(N, K, group_size, nullptr, nullptr);
+  if (st) return st;
+  if (!aligned(packed_r, 16) || !aligned(scales_r, 2)) return fail(KF_ERR_INVALID_ARG, "packed_r / scales_r misaligned");
+  return gemm_entry(x, packed, scales, packed_r, scales_r, y, ws, ws_bytes, M, N, K, group_size, stream);
 }
 
 int kf_int4_quantize(const void* w, int dtype, void* packed, void* scales, int N, int K, int group_size,

@@ -722,8 +722,13 @@ size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
 }
 
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
-                       void* ws, int M, int N, int K, int group_size, hipStream_t stream) {
-  if (p.skinny) return skinny_launch(p.sk, x, packed, scales, y, M, N, K, group_size, stream);
+                       void* ws, int M, int N, int K, int group_size, hipStream_t stream, const void* packed_r,
+                       const void* scales_r) {
+  if (p.skinny) {
+    const bool blocked = packed_r != nullptr && scales_r != nullptr;
+    return skinny_launch(p.sk, x, blocked ? packed_r : packed, blocked ? scales_r : scales, y, M, N, K, group_size,
+                         blocked, stream);
+  }
   const TileEntry& e = kTiles[p.tile];
   const int log2_group = group_size == 128 ? 7 : 6;
   const int tiles_m = ceil_div(M, e.bm);

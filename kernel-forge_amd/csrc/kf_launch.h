@@ -50,7 +50,12 @@ struct SkinnyPlan {
 };
 SkinnyPlan skinny_plan(int M, int N, int K, int cu_count);
 hipError_t skinny_launch(const SkinnyPlan& p, const void* x, const void* packed, const void* scales, void* y, int M,
-                         int N, int K, int group_size, hipStream_t stream);
+                         int N, int K, int group_size, bool blocked, hipStream_t stream);
+// MFMA-16 block copy of packed / scales (kf_skinny.hip): sizes in int32 words and fp16 scales.
+size_t mfma16_packed_words(int N, int K);
+size_t mfma16_scale_count(int N, int K, int group_size);
+hipError_t reorder_mfma16_launch(const void* packed, const void* scales, void* packed_r, void* scales_r, int N, int K,
+                                 int group_size, hipStream_t stream);
 
 // ---- MFMA GEMM (any M, N % 64 == 0) --------------------------------------
 struct GemmPlan {
@@ -67,8 +72,10 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count);
 GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile);
 int gemm_num_tiles();
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N);
+// packed_r / scales_r: the MFMA-16 block copy, read where the skinny kernel runs (may be null).
 hipError_t gemm_launch(const GemmPlan& p, const void* x, const void* packed, const void* scales, void* y,
-                       void* ws, int M, int N, int K, int group_size, hipStream_t stream);
+                       void* ws, int M, int N, int K, int group_size, hipStream_t stream,
+                       const void* packed_r = nullptr, const void* scales_r = nullptr);
 
 // ---- on-device quantize + pack (kf_quant.hip) -------------------------------
 constexpr int kQuantF32 = 0, kQuantF16 = 1, kQuantBF16 = 2;  // == KF_DTYPE_* of the C ABI

@@ -41,6 +41,9 @@ SIGNATURES = {
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm_plan": (_I, [_I, _I, _I, _I, _IP, _IP, _IP, _IP, _IP]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
+    "kf_int4_mfma16_sizes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "kf_int4_reorder_mfma16": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
+    "kf_int4_gemm_mfma16": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
     "kf_int4_dequant_fp16": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP]),
     "kf_int4_quantize": (_I, [_VP, _I, _VP, _VP, _I, _I, _I, _VP]),
     "kf_bw_copy": (_I, [_VP, _VP, _SZ, _I, _VP]),

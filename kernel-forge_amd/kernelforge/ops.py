@@ -99,10 +99,59 @@ def int4_gemv(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group
     return y
 
 
+# The MFMA-16 block copy of a weight (kf_int4_reorder_mfma16) makes the skinny MFMA kernel's
+# weight loads contiguous (7-15% faster at M <= 32) and is bit-identical in results.  When
+# enabled, int4_gemm builds it the first time a weight is used at M <= MFMA16_MAX_M (outside
+# HIP-graph capture) and keeps it on the packed tensor, at the cost of a second copy of that
+# weight in device memory.
+MFMA16_CACHE = True
+MFMA16_MAX_M = 32
+_MFMA16_ATTR = "_kf_mfma16"
+
+
+def int4_reorder_mfma16(packed: torch.Tensor, scales: torch.Tensor,
+                        group_size: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """The MFMA-16 block copy (packed_r int32, scales_r fp16) of a packed weight; K % 128 == 0.
+
+    An internal layout (the public packed format is unchanged); kernel csrc/kf_skinny.hip.
+    """
+    if packed.dtype != torch.int32 or scales.dtype != torch.float16 or not packed.is_cuda:
+        raise TypeError("int4_reorder_mfma16 expects int32 packed and fp16 scales on a CUDA device")
+    if not packed.is_contiguous() or not scales.is_contiguous():
+        raise ValueError("packed and scales must be contiguous")
+    n, k = packed.shape[0], packed.shape[1] * 8
+    lib = _lib.load()
+    pb, sb = ctypes.c_size_t(), ctypes.c_size_t()
+    _lib.check(lib.kf_int4_mfma16_sizes(n, k, int(group_size), ctypes.byref(pb), ctypes.byref(sb)), "mfma16 sizes")
+    packed_r = torch.empty(pb.value // 4, dtype=torch.int32, device=packed.device)
+    scales_r = torch.empty(sb.value // 2, dtype=torch.float16, device=packed.device)
+    with torch.cuda.device(packed.device):
+        _lib.check(lib.kf_int4_reorder_mfma16(_ptr(packed), _ptr(scales), _ptr(packed_r), _ptr(scales_r), n, k,
+                                              int(group_size), _stream_ptr(packed.device)), "int4_reorder_mfma16")
+    return packed_r, scales_r
+
+
+def _mfma16_copy(packed: torch.Tensor, scales: torch.Tensor, group_size: int, m: int):
+    """The cached MFMA-16 copy of (packed, scales), built on first use; None when not applicable."""
+    if not MFMA16_CACHE or m > MFMA16_MAX_M or packed.shape[1] % 16 != 0:
+        return None
+    key = (int(group_size), packed.data_ptr(), packed._version, scales.data_ptr(), scales._version)
+    cached = getattr(packed, _MFMA16_ATTR, None)
+    if cached is not None and cached[0] == key:
+        return cached[1], cached[2]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    if gemm_plan(m, packed.shape[0], packed.shape[1] * 8, group_size, packed.device)["kernel"] != "skinny":
+        return None  # only the skinny kernel reads the copy
+    packed_r, scales_r = int4_reorder_mfma16(packed, scales, group_size)
+    setattr(packed, _MFMA16_ATTR, (key, packed_r, scales_r))
+    return packed_r, scales_r
+
+
 def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """Fused INT4 dequant GEMM on the MFMA matrix cores, any M, N a multiple of 64.
 
-    Reference kernelforge/ops.py:196-201; kernel csrc/kf_gemm.hip.
+    Reference kernelforge/ops.py:196-201; kernels csrc/kf_gemm.hip, csrc/kf_skinny.hip.
     """
     _check_int4(x, packed, scales, group_size)
     if packed.shape[0] % 64 != 0:
@@ -115,9 +164,15 @@ def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group
     with torch.cuda.device(x.device):
         ws_bytes = lib.kf_int4_gemm_workspace_bytes(m, n, k, int(group_size))
         ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=x.device) if ws_bytes else None
-        status = lib.kf_int4_gemm(_ptr(x), _ptr(packed), _ptr(scales), _ptr(y),
-                                  _ptr(ws) if ws is not None else None, ws_bytes, m, n, k, int(group_size),
-                                  _stream_ptr(x.device))
+        copy = _mfma16_copy(packed, scales, group_size, m)
+        if copy is not None:
+            status = lib.kf_int4_gemm_mfma16(_ptr(x), _ptr(packed), _ptr(scales), _ptr(copy[0]), _ptr(copy[1]),
+                                             _ptr(y), _ptr(ws) if ws is not None else None, ws_bytes, m, n, k,
+                                             int(group_size), _stream_ptr(x.device))
+        else:
+            status = lib.kf_int4_gemm(_ptr(x), _ptr(packed), _ptr(scales), _ptr(y),
+                                      _ptr(ws) if ws is not None else None, ws_bytes, m, n, k, int(group_size),
+                                      _stream_ptr(x.device))
     _lib.check(status, "int4_gemm")
     return y
 

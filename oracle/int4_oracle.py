@@ -21,6 +21,10 @@ linear_ref_f64              csrc/micro/sanitize_gemm.cu:58-66
 lcg_workload                csrc/micro/sanitize_gemm.cu:21-50
 max_rel_err                 tests/test_gemm.py:36-45
 algorithmic_bytes / flops   bench/bench_gemm.py:80,98; bench_utils.py:209-210
+reorder_mfma16              no reference function: the layout contract of
+                            kf_int4_reorder_mfma16 (include/kf_int4.h), the
+                            weight copy the reference names as its next step
+                            (docs/phase4-notes.md:59)
 ==========================  ===============================================
 
 How each function is pinned (tests/test_oracle.py):
@@ -41,6 +45,11 @@ How each function is pinned (tests/test_oracle.py):
 * linear_ref_fp32 / linear_ref_f64: against each other and against a brute
   force triple loop on tiny shapes, plus linearity in x.
 * lcg_workload: against the C restatement bit for bit.
+* reorder_mfma16: against a per-element loop that follows the header's wording
+  (lane l of block (b, s): row 16b + l%16, words 16s + 4(l/16) .. +3), and as a
+  permutation (every piece of the source appears, the padded rows repeat row
+  N-1); on the GPU, the GEMM reading the copy equals the GEMM reading the
+  public layout bit for bit.
 """
 
 from __future__ import annotations
@@ -228,3 +237,24 @@ def algorithmic_bytes(m: int, n: int, k: int, group_size: int) -> int:
 def gemm_flops(m: int, n: int, k: int) -> int:
     """kernelforge/bench_utils.py:209-210."""
     return 2 * m * n * k
+
+
+def reorder_mfma16(packed: np.ndarray, scales: np.ndarray, group_size: int) -> tuple[np.ndarray, np.ndarray]:
+    """Layout contract of kf_int4_reorder_mfma16 (include/kf_int4.h); no reference counterpart.
+
+    packed int32 [N, K/8], scales fp16 [N, K/G] -> (packed_r int32 [ceil(N/16) * 16 * K/8],
+    scales_r fp16 [ceil(N/16) * 16 * K/G]).  Pieces of 4 words in order (block b, super-step s,
+    lane l): row min(16b + l%16, N-1), words 16s + 4(l/16) .. +3.  Scales in order (b, group j,
+    column c): scales[min(16b + c, N-1), j].
+    """
+    n, kw = packed.shape
+    k = kw * 8
+    if k % 128 or group_size not in SUPPORTED_GROUP_SIZES:
+        raise ValueError("reorder_mfma16 needs K % 128 == 0 and G in (64, 128)")
+    nb, nss = -(-n // 16), k // 128
+    rows = np.minimum(np.arange(nb * 16), n - 1)
+    p = packed[rows].reshape(nb, 16, nss, 4, 4)           # [b, col, s, g, word]
+    packed_r = np.ascontiguousarray(p.transpose(0, 2, 3, 1, 4)).reshape(-1)  # [b, s, g, col, word]
+    sc = scales[rows].reshape(nb, 16, k // group_size)      # [b, col, j]
+    scales_r = np.ascontiguousarray(sc.transpose(0, 2, 1)).reshape(-1)       # [b, j, col]
+    return packed_r, scales_r

@@ -311,3 +311,43 @@ def test_algorithmic_bytes_formula():
     assert sum(o.algorithmic_bytes(1, n, k, 128) for n, k in tl) == kat["tinyllama_7"]
     assert sum(o.algorithmic_bytes(1, n, k, 128) for n, k in qw) == kat["qwen_7"]
     assert o.gemm_flops(2048, 5632, 2048) == kat["gate_m2048_flops"]
+
+
+@pytest.mark.parametrize("n,k,g", [(1, 128, 128), (16, 256, 64), (37, 384, 128), (40, 256, 64)])
+def test_reorder_mfma16_by_definition(n, k, g):
+    """The layout of kf_int4_reorder_mfma16 element by element, as the header states it."""
+    rng = np.random.default_rng(n * 7 + k)
+    packed = rng.integers(-2**31, 2**31, size=(n, k // 8), dtype=np.int64).astype(np.int32)
+    scales = rng.standard_normal((n, k // g)).astype(np.float16)
+    pr, sr = o.reorder_mfma16(packed, scales, g)
+    nb, nss = -(-n // 16), k // 128
+    assert pr.shape == (nb * 16 * k // 8,) and sr.shape == (nb * 16 * k // g,)
+    piece = 0
+    for b in range(nb):
+        for s in range(nss):
+            for lane in range(64):
+                row = min(16 * b + lane % 16, n - 1)
+                w0 = 16 * s + 4 * (lane // 16)
+                assert np.array_equal(pr[4 * piece:4 * piece + 4], packed[row, w0:w0 + 4])
+                piece += 1
+    i = 0
+    for b in range(nb):
+        for j in range(k // g):
+            for c in range(16):
+                assert sr[i].view(np.uint16) == scales[min(16 * b + c, n - 1), j].view(np.uint16)
+                i += 1
+
+
+def test_reorder_mfma16_is_a_permutation():
+    """Every 4-word piece of the source appears; padding only repeats row N-1."""
+    n, k = 21, 512
+    packed = np.arange(n * k // 8, dtype=np.int32).reshape(n, k // 8)  # every word distinct
+    scales = np.arange(n * k // 128, dtype=np.float16).reshape(n, k // 128)
+    pr, _ = o.reorder_mfma16(packed, scales, 128)
+    pieces = pr.reshape(-1, 4)
+    assert (pieces[:, 1:] == pieces[:, :1] + np.arange(1, 4)).all()  # pieces are whole aligned runs
+    assert set(pieces[:, 0] // 4) == set(range(n * k // 32))          # every source piece present
+    counts = np.bincount(pieces[:, 0] // 4 // (k // 32))
+    assert (counts[:-1] == k // 32).all() and counts[-1] == (32 - n + 1) * (k // 32)  # rows 21..31 repeat row 20
+    with pytest.raises(ValueError):
+        o.reorder_mfma16(packed[:, :12], scales[:, :1], 128)  # K = 96
