@@ -208,6 +208,29 @@ def test_gemm_n_multiple_of_64_not_128(error_log, n):
     _check(error_log, "int4_gemm", ops.int4_gemm, 37, n, 512, 64, f"n{n}")
 
 
+# Ragged shapes that reach every tile-table kernel, with and without split-K: N not a multiple
+# of the tile width, M just past a tile boundary, K % 256 != 0 (no 256-k-stage tile) and
+# K % 128 != 0.  (M, N, K) -> kernel/splits as the dispatcher picks them on 256 CUs.
+EDGE_CASES = [(513, 2112, 384), (1000, 320, 4224), (1000, 2112, 384), (1500, 640, 8960), (33, 64, 1152),
+              (33, 320, 4224), (300, 960, 2048), (33, 192, 2304), (33, 640, 8960), (47, 704, 5120),
+              (130, 1600, 640), (65, 192, 4160)]
+
+
+@pytest.mark.parametrize("m,n,k", EDGE_CASES)
+@pytest.mark.parametrize("group", [64, 128])
+def test_gemm_edge_shapes_every_tile(error_log, m, n, k, group):
+    if k % group:
+        pytest.skip("K not a multiple of the group")
+    _check(error_log, "int4_gemm", ops.int4_gemm, m, n, k, group, f"edge_{m}x{n}x{k}")
+
+
+def test_edge_shapes_reach_every_tile_and_split():
+    plans = [ops.gemm_plan(m, n, k, 64) for m, n, k in EDGE_CASES]
+    num = plans[0]["num_kernels"]
+    assert {p["kernel"] for p in plans} == set(range(num))
+    assert {p["kernel"] for p in plans if p["splits"] > 1} >= {1, 2, 3, 5}
+
+
 @pytest.mark.parametrize("m", [1, 8, 9, 128])
 def test_matmul_dispatcher(error_log, m):
     _check(error_log, "int4_matmul", ops.int4_matmul, m, 2048, 2048, 128, "dispatch")
