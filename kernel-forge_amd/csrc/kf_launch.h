@@ -34,7 +34,7 @@ constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
 
 struct GemvPlan {
   int rows_per_wave;   // R: output rows one wavefront owns
-  int unroll;          // U: 32-k chunks per lane kept in flight per pass
+  int unroll;          // U: 64-chunk blocks (64 lanes x 32 k) whose loads one pass keeps in flight
 };
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
@@ -68,7 +68,8 @@ struct GemmPlan {
   int kt_per_split;// k stages (of the tile's stage depth) per split
 };
 GemmPlan gemm_plan(int M, int N, int K, int cu_count);
-// Plan with an explicit tile-table entry (used by the measured dispatcher table and tuning).
+// Plan with an explicit tile-table entry and the fill-the-CUs split rule (the K % 128 != 0
+// fallback of gemm_plan, and tuning).
 GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile);
 int gemm_num_tiles();
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N);

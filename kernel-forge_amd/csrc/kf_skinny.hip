@@ -1,4 +1,4 @@
-// "Skinny" INT4 GEMM for small M (M <= 64) on gfx950: a weight stream with matrix-core math.
+// "Skinny" INT4 GEMM for small M (M <= 32) on gfx950: a weight stream with matrix-core math.
 //
 // y[M, N] = x[M, K] @ W_hat^T with W_hat = fp16_rne(q * s) (the same operand the tiled GEMM
 // and the reference's tensor-core kernel use, dequant_gemm_tc_kernel.cuh:100-112), fp32

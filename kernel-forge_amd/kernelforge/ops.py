@@ -131,21 +131,39 @@ def int4_reorder_mfma16(packed: torch.Tensor, scales: torch.Tensor,
     return packed_r, scales_r
 
 
+def _mfma16_key(packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> tuple:
+    """What the cached copy must match.  Tensors made under torch.inference_mode() keep no
+    version counter, so an in-place update of them cannot be seen: their key has no versions."""
+    versions = None if packed.is_inference() or scales.is_inference() else (packed._version, scales._version)
+    return (int(group_size), packed.data_ptr(), scales.data_ptr(), versions)
+
+
+def prepare_mfma16(packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> None:
+    """Builds the MFMA-16 copy of a weight now and keeps it on `packed` for int4_gemm.
+
+    int4_gemm builds it by itself on first use, except for tensors created under
+    torch.inference_mode() (no version counter to notice in-place updates): for those this is
+    the only way, and the caller promises not to modify packed / scales in place afterwards.
+    """
+    packed_r, scales_r = int4_reorder_mfma16(packed, scales, group_size)
+    setattr(packed, _MFMA16_ATTR, (_mfma16_key(packed, scales, group_size), packed_r, scales_r))
+
+
 def _mfma16_copy(packed: torch.Tensor, scales: torch.Tensor, group_size: int, m: int):
     """The cached MFMA-16 copy of (packed, scales), built on first use; None when not applicable."""
     if not MFMA16_CACHE or m > MFMA16_MAX_M or packed.shape[1] % 16 != 0:
         return None
-    key = (int(group_size), packed.data_ptr(), packed._version, scales.data_ptr(), scales._version)
+    key = _mfma16_key(packed, scales, group_size)
     cached = getattr(packed, _MFMA16_ATTR, None)
     if cached is not None and cached[0] == key:
         return cached[1], cached[2]
-    if torch.cuda.is_current_stream_capturing():
-        return None
+    if key[3] is None or torch.cuda.is_current_stream_capturing():
+        return None  # inference tensors: only a copy made by prepare_mfma16
     if gemm_plan(m, packed.shape[0], packed.shape[1] * 8, group_size, packed.device)["kernel"] != "skinny":
         return None  # only the skinny kernel reads the copy
-    packed_r, scales_r = int4_reorder_mfma16(packed, scales, group_size)
-    setattr(packed, _MFMA16_ATTR, (key, packed_r, scales_r))
-    return packed_r, scales_r
+    prepare_mfma16(packed, scales, group_size)
+    cached = getattr(packed, _MFMA16_ATTR)
+    return cached[1], cached[2]
 
 
 def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:

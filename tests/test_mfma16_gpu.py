@@ -146,3 +146,18 @@ def test_mfma16_rejections():
     assert lib.kf_int4_reorder_mfma16(dp.data_ptr(), ds.data_ptr(), None, None, 64, 256, 128, stream) != 0
     with pytest.raises(TypeError):
         ops.int4_reorder_mfma16(dp.float(), ds, 128)
+
+
+def test_inference_mode_weights_use_only_a_prepared_copy():
+    """Inference tensors carry no version counter: no implicit copy; prepare_mfma16 opts in."""
+    n, k, g = 2048, 2048, 128
+    packed, scales, _, _ = _weight(n, k, g)
+    with torch.inference_mode():
+        dp = torch.from_numpy(packed).to(DEV)
+        ds = torch.from_numpy(scales).to(DEV)
+        x = torch.randn(8, k, device=DEV).half()
+        plain = ops.int4_gemm(x, dp, ds, g)
+        assert getattr(dp, "_kf_mfma16", None) is None
+        ops.prepare_mfma16(dp, ds, g)
+        assert getattr(dp, "_kf_mfma16", None) is not None
+        assert torch.equal(ops.int4_gemm(x, dp, ds, g), plain)
