@@ -359,23 +359,40 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
 // three slabs of 4-byte slots, one slab per group, fetched by the k-group 0 wavefronts with
 // the first stage of the group: a stage that starts a group costs those two wavefronts one
 // more DMA, and their wait count for it is one higher.
-namespace dma {
-constexpr int BM = 128, BN = 128, BK = 64, NS = 3, THREADS = 256;
-constexpr int TM = 8, TN = 4;
-constexpr int A_ROW = BK * 2;              // 128 B
-constexpr int A_BYTES = BM * A_ROW;        // 16384
-constexpr int B_OFF = A_BYTES;
-constexpr int B_ROW = BK / 2;              // 32 B
-constexpr int B_BYTES = BN * B_ROW;        // 4096
-constexpr int STAGE = B_OFF + B_BYTES;     // 20480
-constexpr int S_RING = NS * STAGE;         // scale slabs after the stages: [NS][BN] 4-byte slots
-constexpr int S_SLAB = BN * 4;
-constexpr int OUT_ROW = BN * 2 + 16;       // epilogue fp16 tile row stride (bytes), padded
-constexpr int RED_BYTES = 2 * TM * TN * 256 * 4;  // k-group 1's partial tiles (2 wavefronts)
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
-constexpr int SMEM = cmax(cmax(S_RING + NS * S_SLAB, RED_BYTES), BM * OUT_ROW);  // epilogue reuses it
-constexpr int kDmaPerStage = 5;            // per wavefront: 4 x, 1 packed (+1 scales, see below)
-}  // namespace dma
+// Constants of the DMA-fed kernel with KW k-groups (KW = 2: 4 wavefronts, 64-k stages;
+// KW = 4: 8 wavefronts, 128-k stages).  Every wavefront owns a 128 x 64 wave tile over a 32-k
+// slice of each stage, so the VALU/MFMA and LDS/MFMA ratios are the same for both; KW = 4 puts
+// two wavefronts per SIMD into one workgroup per CU, for grids with about one tile per CU.
+template <int KW>
+struct DmaCfg {
+  static constexpr int BM = 128, BN = 128, BK = 32 * KW, NS = 3, WAVES = 2 * KW, THREADS = 64 * WAVES;
+  static constexpr int TM = 8, TN = 4;
+  static constexpr int A_ROW = BK * 2;               // bytes of x per row and stage (128 / 256)
+  static constexpr int A_CH = BK / 8;                // 16-byte chunks per x row (8 / 16)
+  static constexpr int A_RSH = A_ROW >= 256 ? 0 : 1; // rows per 256-byte bank window: 1 or 2
+  static constexpr int A_BYTES = BM * A_ROW;
+  static constexpr int B_OFF = A_BYTES;
+  static constexpr int B_ROW = BK / 2;               // bytes of packed weights per row and stage
+  static constexpr int B_CH = BK / 32;               // 16-byte chunks per packed row (2 / 4)
+  static constexpr int B_BYTES = BN * B_ROW;
+  // Scales.  KW = 2: a stage lies inside one group (G >= 64 = BK), so the scales live in a ring
+  // of NS per-group slabs after the stages and are fetched once per group.  KW = 4: a stage
+  // holds one (G = 128) or two (G = 64) groups, fetched with the stage into its own slabs.
+  static constexpr bool STAGE_SCALES = KW == 4;
+  static constexpr int S_SLAB = BN * 4;              // [BN] 4-byte slots
+  static constexpr int S_OFF = B_OFF + B_BYTES;      // per-stage slabs (KW = 4): [2][BN]
+  static constexpr int STAGE = STAGE_SCALES ? S_OFF + 2 * S_SLAB : S_OFF;
+  static constexpr int S_RING = NS * STAGE;          // per-group ring (KW = 2): [NS][BN]
+  static constexpr int RING_END = S_RING + (STAGE_SCALES ? 0 : NS * S_SLAB);
+  static constexpr int OUT_ROW = BN * 2 + 16;        // epilogue fp16 tile row stride (bytes), padded
+  static constexpr int WAVE_TILE = TM * TN * 256 * 4;  // fp32 partial tile of one wavefront
+  static constexpr int RED_BYTES = (KW / 2) * 2 * WAVE_TILE;  // k-group partials staged at once
+  static constexpr int SMEM = RING_END > RED_BYTES ? (RING_END > BM * OUT_ROW ? RING_END : BM * OUT_ROW)
+                                                   : (RED_BYTES > BM * OUT_ROW ? RED_BYTES : BM * OUT_ROW);
+  static constexpr int kDmaPerStage = 5;             // per wavefront: 4 x, 1 packed (+1 scales, see below)
+  static_assert(A_BYTES == 4 * 1024 * WAVES && B_BYTES == 1024 * WAVES, "4 x and 1 packed DMA per wavefront");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+};
 
 __device__ __forceinline__ void dma_16B(uint32_t lds, const void* src) {
   asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lds), "v"(src) : "memory");
@@ -384,13 +401,17 @@ __device__ __forceinline__ void dma_u16(uint32_t lds, const void* src) {
   asm volatile("global_load_lds_ushort %1, off" ::"{m0}"(lds), "v"(src) : "memory");
 }
 
-__global__ __launch_bounds__(dma::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int KW>
+__global__ __launch_bounds__(DmaCfg<KW>::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
                      const half_t* __restrict__ scales, half_t* __restrict__ y, float* __restrict__ ws, int M, int N,
                      int K, int log2_group, int stages_per_split, int splits, int tiles_m, int tiles_n,
                      int group_m) {
-  using namespace dma;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  using C = DmaCfg<KW>;
+  constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NS = C::NS, THREADS = C::THREADS, TM = C::TM, TN = C::TN;
+  constexpr int A_ROW = C::A_ROW, B_ROW = C::B_ROW, B_OFF = C::B_OFF, STAGE = C::STAGE, OUT_ROW = C::OUT_ROW;
+  constexpr int kDmaPerStage = C::kDmaPerStage;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[C::SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -414,25 +435,31 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   const int last = min(nst, st_begin + stages_per_split) - 1;
   const int ns = last + 1 - st_begin;
 
+  // XOR swizzles: x chunk c of row r at slot c ^ a_swz(r); packed chunk h of row r at h ^ b_swz(r).
+  auto a_swz = [](int row) { return (row >> C::A_RSH) & (C::A_CH - 1); };
+  auto b_swz = [](int row) { return (row / (16 / C::B_CH)) & (C::B_CH - 1); };
+
   // Per-lane DMA sources at k = 0 (advanced by the stage's k offset).  x: this wave's 4
-  // instructions cover rows 32 wave .. +31, 8 rows each, 8 lanes per row.  packed: rows
-  // 32 wave .. +31, 2 lanes per row.  scales: column 64 wn + lane, for k-group kw.
+  // instructions of 1 KiB cover 1024 / A_ROW rows each; packed: one instruction of 1 KiB.
+  constexpr int A_RPI = 1024 / A_ROW, A_LPR = A_ROW / 16;  // rows per instruction, lanes per row
+  constexpr int B_RPI = 1024 / B_ROW, B_LPR = B_ROW / 16;
   const half_t* a_src[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int row = 8 * (4 * wave + q) + (lane >> 3);
-    a_src[q] = x + (size_t)min(m0 + row, M - 1) * K + 8 * ((lane & 7) ^ ((row >> 1) & 7));
+    const int row = A_RPI * (4 * wave + q) + lane / A_LPR;
+    a_src[q] = x + (size_t)min(m0 + row, M - 1) * K + 8 * ((lane % A_LPR) ^ a_swz(row));
   }
-  const int brow = 32 * wave + (lane >> 1);
+  const int brow = B_RPI * wave + lane / B_LPR;
   const uint32_t* b_src =
-      packed + (size_t)min(n0 + brow, N - 1) * (K >> 3) + 4 * ((lane & 1) ^ ((brow >> 3) & 1));
-  const half_t* s_src = scales + (size_t)min(n0 + 64 * wn + lane, N - 1) * (K >> log2_group);
+      packed + (size_t)min(n0 + brow, N - 1) * (K >> 3) + 4 * ((lane % B_LPR) ^ b_swz(brow));
+  const int groups = K >> log2_group;
+  const half_t* s_src = scales + (size_t)min(n0 + 64 * wn + lane, N - 1) * groups;
   const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
 
-  // Split-local stage i (clamped) starts a scale group when i == 0 or its k0 is a multiple
-  // of G; groups are numbered from the split's first stage.  The clamped repeats of the
-  // last stage past the split's end never start one.
-  const int log2_spg = log2_group - 6;  // log2(stages per group)
+  // KW = 2, per-group scale ring: split-local stage i (clamped) starts a scale group when
+  // i == 0 or its k0 is a multiple of G; groups are numbered from the split's first stage.
+  // The clamped repeats of the last stage past the split's end never start one.
+  const int log2_spg = log2_group - 6;  // log2(stages per group), KW = 2
   auto starts_group = [&](int i) {
     const int st = st_begin + i;
     return i == 0 || (st <= last && (st & ((1 << log2_spg) - 1)) == 0);
@@ -440,8 +467,13 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   auto group_of = [&](int i) {  // split-local group index of split-local stage i (i <= ns - 1)
     return ((st_begin + i) >> log2_spg) - (st_begin >> log2_spg);
   };
-  // DMA of split-local stage i (clamped) into buffer i % NS, plus its group's scales.
-  // Returns whether this wavefront issued the scale load (one more outstanding load).
+  // KW = 4, per-stage scales: a stage holds gps = BK / G groups (1 or 2); k-group kw < gps
+  // fetches group gps * st + kw for its wavefronts' 64 columns, and k-group kw reads slab
+  // (32 kw) >> log2_group.
+  const int gps = BK >> log2_group;
+  const bool stage_scale_loader = C::STAGE_SCALES && kw < gps;
+  // DMA of split-local stage i (clamped) into buffer i % NS, plus scales.  Returns whether
+  // this wavefront issued a scale load (one more outstanding load).
   auto issue = [&](int i, int buf) {  // buf == i % NS
     const int st = min(st_begin + i, last);
     const int k0 = st * BK;
@@ -449,13 +481,21 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_16B(base + 1024 * (4 * wave + q), a_src[q] + k0);
     dma_16B(base + B_OFF + 1024 * wave, b_src + (k0 >> 3));
-    const bool sc = kw == 0 && starts_group(i);
-    if (sc) {
-      const uint32_t sbase =
-          __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)(S_RING + (group_of(i) % NS) * S_SLAB + 256 * wn));
-      dma_u16(sbase, s_src + (k0 >> log2_group));
+    if constexpr (C::STAGE_SCALES) {
+      if (stage_scale_loader) {
+        dma_u16(__builtin_amdgcn_readfirstlane(base + (uint32_t)(C::S_OFF + kw * C::S_SLAB + 256 * wn)),
+                s_src + gps * st + kw);
+      }
+      return stage_scale_loader;
+    } else {
+      const bool sc = kw == 0 && starts_group(i);
+      if (sc) {
+        const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+            smem_base + (uint32_t)(C::S_RING + (group_of(i) % NS) * C::S_SLAB + 256 * wn));
+        dma_u16(sbase, s_src + (k0 >> log2_group));
+      }
+      return sc;
     }
-    return sc;
   };
   auto wait_older = [&](bool newer_has_scales) {  // all but the newest stage's loads landed
     if (newer_has_scales)
@@ -471,10 +511,10 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
     for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   // Lane-dependent LDS offsets inside a stage.  x: row l16 (+16 per block), chunk 4 kw + g.
-  // packed: row 64 wn + 16 j + l16, dword 4 kw + g.  scales: [kw][64 wn + 16 j + l16].
-  const int a_off = l16 * A_ROW + 16 * ((4 * kw + g) ^ ((l16 >> 1) & 7));
-  const int b_off = B_OFF + (64 * wn + l16) * B_ROW + 16 * (kw ^ ((l16 >> 3) & 1)) + 4 * g;
-  const int s_off = 4 * (64 * wn + l16);  // within a scale slab
+  // packed: row 64 wn + 16 j + l16, dword 4 kw + g.  scales: column 64 wn + 16 j + l16.
+  const int a_off = l16 * A_ROW + 16 * ((4 * kw + g) ^ a_swz(l16));
+  const int b_off = B_OFF + (64 * wn + l16) * B_ROW + 16 * (kw ^ b_swz(l16)) + 4 * g;
+  const int s_off = 4 * (64 * wn + l16) + (C::STAGE_SCALES ? C::S_OFF + ((32 * kw) >> log2_group) * C::S_SLAB : 0);
 
   const UnpackConsts uc = unpack_consts();
   half8_t a[TM];
@@ -482,7 +522,7 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   half2_t s2[TN];
   auto read_frags = [&](int i, int buf) {  // buf == i % NS, a compile-time constant at the call
     const unsigned char* st = smem + buf * STAGE;
-    const unsigned char* slab = smem + S_RING + (group_of(i) % NS) * S_SLAB;
+    const unsigned char* slab = C::STAGE_SCALES ? st : smem + C::S_RING + (group_of(i) % NS) * C::S_SLAB;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       w[j] = *reinterpret_cast<const uint32_t*>(st + b_off + 16 * B_ROW * j);
@@ -497,9 +537,9 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   // wavefront waits for its own loads of it and the barrier publishes it; at iteration i
   // its fragments are read and its MFMAs run.  The DMA of stage i + 2 (iteration i)
   // overwrites the buffer of stage i - 1, whose reads completed before the barrier of
-  // iteration i - 1 (lgkmcnt(0) precedes every barrier).  Likewise the scale slab of group
-  // q is fetched with q's first stage i (iteration i - 2) into the slab of group q - 3,
-  // last read at a stage <= i - 3 (groups span >= 1 stage), before that barrier.
+  // iteration i - 1 (lgkmcnt(0) precedes every barrier).  Likewise (KW = 2) the scale slab
+  // of group q is fetched with q's first stage i (iteration i - 2) into the slab of group
+  // q - 3, last read at a stage <= i - 3 (groups span >= 1 stage), before that barrier.
   // The loop is unrolled by NS so every buffer offset is a compile-time immediate.
   issue(0, 0);
   wait_older(issue(1, 1));
@@ -527,22 +567,32 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped tail loads, before LDS is reused
   __syncthreads();
 
-  // k-group 1 hands its partial tiles to k-group 0, which adds them (fixed order).
+  // The k-groups' partial tiles are added in fixed order through LDS: KW = 2: a0 + a1;
+  // KW = 4: (a0 + a2) + (a1 + a3).  Round r hands k-group giver's tile to k-group taker through
+  // slot h (one 2 x wave-tile region per slot); straight-line code keeps acc in registers.
   float* red = reinterpret_cast<float*>(smem);
-  if (kw == 1) {
+  constexpr int ROUNDS = KW == 4 ? 2 : 1;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int r = 0; r < ROUNDS; ++r) {
+    const bool last_round = r == ROUNDS - 1;
+    const bool give = last_round ? kw == 1 : kw >= 2;
+    const bool take = last_round ? kw == 0 : kw < 2;
+    const int h = last_round ? 0 : (kw & 1);
+    float* base = red + ((h * 2 + wn) * TM * TN) * 256 + 4 * lane;
+    if (r > 0) __syncthreads();  // the previous round's tiles have been read
+    if (give) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        *reinterpret_cast<float4_t*>(&red[((wn * TM + i) * TN + j) * 256 + 4 * lane]) = acc[i][j];
-  }
-  __syncthreads();
-  if (kw == 0) {
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) *reinterpret_cast<float4_t*>(base + (i * TN + j) * 256) = acc[i][j];
+    }
+    __syncthreads();
+    if (take) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] += *reinterpret_cast<const float4_t*>(&red[((wn * TM + i) * TN + j) * 256 + 4 * lane]);
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += *reinterpret_cast<const float4_t*>(base + (i * TN + j) * 256);
+    }
   }
 
   // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
@@ -563,7 +613,7 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
     }
     return;
   }
-  // fp16 tile through LDS, then 16-byte row-major stores by all four wavefronts.
+  // fp16 tile through LDS, then 16-byte row-major stores by all wavefronts.
   __syncthreads();  // the partial tiles have been read
   if (kw == 0) {
 #pragma unroll
@@ -615,20 +665,21 @@ TileEntry entry(int blocks_per_cu, double us_per_gmac, double us_fixed) {
 
 // Tile table: index = GemmPlan::tile.  Cost terms: least-squares fit (log-time) of the model
 // in gemm_plan to graph-replayed timings of every tile and split count over the TinyLlama and
-// Qwen2.5 layer shapes, M = 16 .. 4096, on MI355X (3,460 points, rms error 7.0%).
+// Qwen2.5 layer shapes, M = 16 .. 4096, on MI355X (4,172 points, rms error 7.0%).
 const TileEntry kTiles[] = {
     entry<TileCfg<64, 128, 1, 4, 1>>(0, 0.0, 0.0),         // 0: 64 x 128, 4 waves; 64-k stages (any K)
-    entry<TileCfg<64, 128, 1, 4, 2>>(1, 625.47, 3.039),    // 1: 64 x 128, 8 waves (2 k-groups)
-    TileEntry{dma::BM, dma::BN, dma::BK, dma::THREADS, 2, 538.68, 5.589, gemm_dma_kernel},  // 2: DMA 128 x 128
-    entry<TileCfg<32, 128, 1, 4, 2>>(1, 906.11, 2.112),    // 3: 32 x 128, 8 waves (2 k-groups)
-    entry<TileCfg<32, 64, 1, 2, 4>>(1, 1032.15, 2.504),    // 4: 32 x 64, 8 waves (4 k-groups, 256-k stages)
-    entry<TileCfg<16, 64, 1, 2, 4>>(1, 1761.05, 1.935),    // 5: 16 x 64, 8 waves (4 k-groups, 256-k stages)
+    entry<TileCfg<64, 128, 1, 4, 2>>(1, 630.70, 2.863),    // 1: 64 x 128, 8 waves (2 k-groups)
+    TileEntry{128, 128, DmaCfg<2>::BK, DmaCfg<2>::THREADS, 2, 543.09, 5.333, gemm_dma_kernel<2>},  // 2: DMA 128 x 128
+    entry<TileCfg<32, 128, 1, 4, 2>>(1, 915.33, 1.981),    // 3: 32 x 128, 8 waves (2 k-groups)
+    entry<TileCfg<32, 64, 1, 2, 4>>(1, 1036.37, 2.430),    // 4: 32 x 64, 8 waves (4 k-groups, 256-k stages)
+    entry<TileCfg<16, 64, 1, 2, 4>>(1, 1760.44, 1.894),    // 5: 16 x 64, 8 waves (4 k-groups, 256-k stages)
+    TileEntry{128, 128, DmaCfg<4>::BK, DmaCfg<4>::THREADS, 1, 375.53, 6.692, gemm_dma_kernel<4>},  // 6: DMA, 8 waves
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 constexpr int kTile64 = 0, kDmaTile = 2;
 // Split-K costs one more launch plus the fp32 partials: kSplitUs + kSplitUsPerElem * splits * M * N
 // (same fit), and is taken only when the model predicts it at least 10% faster.
-constexpr double kSplitUs = 2.786, kSplitUsPerElem = 1.5147e-6, kSplitMargin = 0.9;
+constexpr double kSplitUs = 2.924, kSplitUsPerElem = 1.5826e-6, kSplitMargin = 0.9;
 constexpr int kMaxSplits = 12;  // the largest split count the fit was measured on
 
 GemmPlan plan_for(int K, int tile, int splits) {
@@ -685,7 +736,7 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
     return p;
   }
   if (!k128) {  // K % 64 == 0 only: the 64-k-stage kernels
-    const long dma_tiles = (long)ceil_div(M, dma::BM) * ceil_div(N, dma::BN);
+    const long dma_tiles = (long)ceil_div(M, 128) * ceil_div(N, 128);
     return gemm_plan_with_tile(M, N, K, cu_count, dma_tiles >= cus ? kDmaTile : kTile64);
   }
   int best_tile = kDmaTile, best_splits = 1;

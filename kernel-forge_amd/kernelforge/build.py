@@ -10,6 +10,7 @@ into ``kernelforge/libkf_int4.so``, where ``kernelforge._lib`` loads it.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -44,22 +45,44 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the MI355X library needs ROCm's hipcc to build")
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str], quiet_remarks: bool = False) -> str:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that noise.
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
-    if err.strip():
-        print(err, file=sys.stderr)
+    shown = err
+    if quiet_remarks:
+        shown = "\n".join(line for line in err.splitlines()
+                          if "kernel-resource-usage" not in line and not line.lstrip().startswith(("|", "^"))
+                          and not line.lstrip()[:1].isdigit())
+    if shown.strip():
+        print(shown, file=sys.stderr)
+    return err
+
+
+def _check_resources(remarks: str, src: str) -> None:
+    """Every kernel must run from registers: no scratch (private segment) and no spills.  A
+    kernel whose accumulators fall to scratch still gives right answers, 10-20x slower."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"(ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill): (\d+)", line)
+        if m and int(m.group(2)) > 0:
+            bad.append(f"{name}: {m.group(1)} = {m.group(2)}")
+    if bad:
+        raise RuntimeError(f"{src}: kernels use scratch memory or spill registers:\n  " + "\n  ".join(bad))
 
 
 def build_library(verbose: bool = False, resource_usage: bool = False) -> Path:
     """Compiles every kernel source and links libkf_int4.so; returns its path."""
     cc = hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    extra = ["-Rpass-analysis=kernel-resource-usage"] if resource_usage else []
+    extra = ["-Rpass-analysis=kernel-resource-usage"]
 
     def compile_one(src: str) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
@@ -67,7 +90,8 @@ def build_library(verbose: bool = False, resource_usage: bool = False) -> Path:
                "-c", str(SRC_DIR / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
-        _run(cmd)
+        remarks = _run(cmd, quiet_remarks=not resource_usage)
+        _check_resources(remarks, src)
         return obj
 
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 4)) as pool:

@@ -213,7 +213,7 @@ def test_gemm_n_multiple_of_64_not_128(error_log, n):
 # K % 128 != 0.  (M, N, K) -> kernel/splits as the dispatcher picks them on 256 CUs.
 EDGE_CASES = [(513, 2112, 384), (1000, 320, 4224), (1000, 2112, 384), (1500, 640, 8960), (33, 64, 1152),
               (33, 320, 4224), (300, 960, 2048), (33, 192, 2304), (33, 640, 8960), (47, 704, 5120),
-              (130, 1600, 640), (65, 192, 4160)]
+              (130, 1600, 640), (65, 192, 4160), (900, 1472, 6272), (600, 1216, 7424)]
 
 
 @pytest.mark.parametrize("m,n,k", EDGE_CASES)
@@ -228,7 +228,7 @@ def test_edge_shapes_reach_every_tile_and_split():
     plans = [ops.gemm_plan(m, n, k, 64) for m, n, k in EDGE_CASES]
     num = plans[0]["num_kernels"]
     assert {p["kernel"] for p in plans} == set(range(num))
-    assert {p["kernel"] for p in plans if p["splits"] > 1} >= {1, 2, 3, 5}
+    assert {p["kernel"] for p in plans if p["splits"] > 1} >= {1, 2, 3, 5, 6}
 
 
 @pytest.mark.parametrize("m", [1, 8, 9, 128])
@@ -244,8 +244,9 @@ def test_gemm_rejects_n_not_multiple_of_64():
 
 
 @pytest.mark.parametrize("layer,m,splitk", [("tinyllama_kv", 128, False), ("tinyllama_down", 64, True),
-                                             ("qwen_down", 32, True), ("tinyllama_down", 2048, True),
-                                             ("tinyllama_gate_up", 16, False), ("tinyllama_gate_up", 768, False)])
+                                             ("qwen_down", 32, True), ("tinyllama_down", 2048, False),
+                                             ("qwen_down", 1536, True), ("tinyllama_gate_up", 16, False),
+                                             ("tinyllama_gate_up", 768, False)])
 def test_gemm_is_deterministic(layer, m, splitk):
     """Split-K partials, the DMA kernel's in-block k-group halves and the skinny kernel's
     per-wave K slices are reduced in fixed order: repeated calls are bitwise identical."""
@@ -264,14 +265,14 @@ def test_dispatcher_covers_every_gemm_kernel():
     cases = [(m, *LAYER_SHAPES[layer]) for layer in LAYER_SHAPES for m in (1, 8, 9, 16, 17, 32, 64, 65, 128)]
     cases += [(m, *LAYER_SHAPES[layer]) for layer in ("tinyllama_gate_up", "tinyllama_down")
               for m in (200, 256, 512, 2048)]
-    cases += [(33, 128, 4160), (65, 192, 512), (17, 5632, 2048), (300, 2048, 5632)]
+    cases += [(33, 128, 4160), (65, 192, 512), (17, 5632, 2048), (300, 2048, 5632), (1536, 1536, 8960)]
     plans = [ops.gemm_plan(m, n, k, 128) for m, n, k in cases]
     kernels = {p["kernel"] for p in plans}
     num = plans[0]["num_kernels"]
     assert kernels == {"skinny", *range(num)}, f"kernels reached: {sorted(map(str, kernels))} of {num} + skinny"
     split_kernels = {p["kernel"] for p in plans if p["splits"] > 1}
-    assert any(p["tile"] == (128, 128) and p["splits"] > 1 for p in plans), "no DMA split-K case"
-    assert any(p["tile"] != (128, 128) and p["splits"] > 1 for p in plans), f"split-K only on {split_kernels}"
+    assert 2 in split_kernels, f"no split-K case for the DMA kernel: {split_kernels}"
+    assert split_kernels - {2, 6}, f"split-K only on the DMA kernels: {split_kernels}"
     for (m, n, k), p in zip(cases, plans):
         ws = _lib.load().kf_int4_gemm_workspace_bytes(m, n, k, 128)
         assert (ws > 0) == (p["splits"] > 1)
