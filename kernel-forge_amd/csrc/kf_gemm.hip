@@ -6,8 +6,14 @@
 // fixed split order (deterministic), the behaviour of the reference's splitk_reduce
 // (dequant_gemm_tc_kernel.cuh:156-162).
 //
-// Design (gfx950: 4 SIMDs per CU, ~2 VALU ops hide under one 16x16x32 MFMA, LDS reads
-// ~150-200 B/clk per CU):
+// Two kernel families share one tile table (kTiles below; gemm_plan picks an entry and a
+// split-K factor with a fitted cost model):
+//   * gemm_kernel<TileCfg>: register-staged LDS tiles, 64 x 128 down to 16 x 64;
+//   * gemm_dma_kernel<KW>: 128 x 128 tiles fed by LDS-DMA, 2 (4 wavefronts) or 4 (8 wavefronts)
+//     k-groups; see the comment above the kernel.
+//
+// Design of gemm_kernel (gfx950: 4 SIMDs per CU, ~2 VALU ops hide under one 16x16x32 MFMA,
+// LDS reads ~150-200 B/clk per CU):
 //   * Workgroup tile BM x BN; WGM x WGN wavefronts tile it, and WK such groups split each
 //     stage's k range (in-block split-K, summed in fixed order through LDS at the end).
 //   * A stage covers SK = 64 * WK k.  x is staged in LDS as fp16; the weights stay PACKED
@@ -330,7 +336,8 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
     }
 }
 
-// ---- DMA-fed kernel: 128 x 128 tile, 4 wavefronts, 64-k stages ------------------------
+// ---- DMA-fed kernel: 128 x 128 tile, KW k-groups (KW = 2: 4 wavefronts, 64-k stages;
+// KW = 4: 8 wavefronts, 128-k stages) ------------------------------------------------
 //
 // Every byte of a stage goes global -> LDS through the gfx950 LDS-DMA loads
 // (global_load_lds_dwordx4 / _ushort: lane l's data lands at M0 + 16 l, or M0 + 4 l for
@@ -341,9 +348,10 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
 // stay well under the LDS bandwidth).
 //
 // Wavefront (kw, wn): column half wn (64 columns) and k-group kw, which takes k 32 kw ..
-// 32 kw + 31 of every 64-k stage; the two k-groups' accumulators are summed in fixed order
-// through LDS at the end (in-block split-K).  Four wavefronts per 128 x 128 tile keep the
-// number of equal wave tasks high enough to spread evenly over the 1024 SIMDs.
+// 32 kw + 31 of every stage; the k-groups' accumulators are summed in fixed order through LDS
+// at the end (in-block split-K).  KW = 2 gives four wave tasks per 128 x 128 tile, enough to
+// spread evenly over the 1024 SIMDs when the grid has several tiles per CU; KW = 4 gives one
+// workgroup of two wavefronts per SIMD when the grid has about one tile per CU.
 //
 // The DMA loads are issued from inline assembly with a "memory" clobber: the compiler
 // neither tracks them nor moves LDS accesses across them, and the loop contains no
@@ -352,13 +360,14 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
 // skipped), so "s_waitcnt vmcnt(kDmaPerStage)" means: the older stage has landed, the
 // newer one may still be in flight.
 //
-// LDS stage layout (bytes): x rows of 128 B (64 k) with 16-byte chunk c at slot
-// c ^ ((row >> 1) & 7); packed rows of 32 B with 16-byte half h at h ^ ((row >> 3) & 1).
-// Every read phase of the MFMA fragments is free of bank conflicts.  Three stages rotate.
-// Scales change once per group (G >= 64 = one stage), so they live in their own ring of
+// LDS stage layout (bytes): x rows of A_ROW = 2 BK bytes with 16-byte chunk c at slot
+// c ^ a_swz(row); packed rows of BK / 2 bytes with 16-byte chunk h at h ^ b_swz(row).  Every
+// read phase of the MFMA fragments is free of bank conflicts.  Three stages rotate.  Scales:
+// with KW = 2 a stage lies inside one group (G >= 64 = BK), so they live in their own ring of
 // three slabs of 4-byte slots, one slab per group, fetched by the k-group 0 wavefronts with
-// the first stage of the group: a stage that starts a group costs those two wavefronts one
-// more DMA, and their wait count for it is one higher.
+// the first stage of the group (that stage costs those two wavefronts one more DMA, and their
+// wait count for it is one higher); with KW = 4 each stage carries the slabs of its one or two
+// groups, fetched by the first one or two k-groups with every stage.
 // Constants of the DMA-fed kernel with KW k-groups (KW = 2: 4 wavefronts, 64-k stages;
 // KW = 4: 8 wavefronts, 128-k stages).  Every wavefront owns a 128 x 64 wave tile over a 32-k
 // slice of each stage, so the VALU/MFMA and LDS/MFMA ratios are the same for both; KW = 4 puts
