@@ -22,19 +22,36 @@ struct GemvProblem {
   int K;
 };
 
+// One problem as the grouped kernel reads it: the problem plus the index of its first
+// wavefront in the launch.
+struct GemvSlot {
+  const void* x;
+  const void* packed;
+  const void* scales;
+  void* y;
+  int N;
+  int K;
+  int wave0;
+  int pad;
+};
+
 // The grouped kernel's arguments: the lookup header as ten scalar arguments (preloaded into
 // SGPRs at wave launch), then this table by value.  A wavefront finds its problem from the
-// header without memory traffic and then fetches that problem's 40-byte descriptor in one
-// round of scalar loads (see kf_gemv.hip).
+// header without memory traffic and then fetches that problem's 48-byte slot in one round of
+// scalar loads (see kf_gemv.hip).
 struct GemvTable {
-  GemvProblem prob[kMaxGemvGroup];
+  GemvSlot slot[kMaxGemvGroup];
 };
 
 constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
+// Largest x (M * K fp16 values, in bytes) a workgroup copies into LDS; 20 KiB keeps eight
+// workgroups (32 wavefronts) per CU within the 160 KiB of LDS.
+constexpr int kGemvMaxLdsX = 20480;
 
 struct GemvPlan {
   int rows_per_wave;   // R: output rows one wavefront owns
   int unroll;          // U: 64-chunk blocks (64 lanes x 32 k) whose loads one pass keeps in flight
+  bool x_lds;          // each workgroup copies x into LDS once (else every lane loads its x)
 };
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
