@@ -85,17 +85,17 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2, const Unpack
   return out;
 }
 
-// Wave64 sum with DPP row ops; the total lands in lane 63.
+// Sum over each 32-lane half of a wave64 with DPP row ops: lane 31 ends with the total of
+// lanes 0-31 and lane 63 with that of lanes 32-63.
 //   quad_perm [1,0,3,2] and [2,3,0,1]: every lane holds its quad's sum
 //   row_shr:4, row_shr:8: lane 15 of each 16-lane row holds the row sum
-//   row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3: lane 63 holds the total
-__device__ __forceinline__ float wave_sum_lane63(float v) {
+//   row_bcast:15 into rows 1 and 3: lanes 31 and 63 hold their half's total
+__device__ __forceinline__ float half_sum_lanes31_63(float v) {
   v += __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0.0f, v, 0x114, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0.0f, v, 0x118, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false);
-  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false);
   return v;
 }
 

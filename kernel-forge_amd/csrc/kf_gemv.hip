@@ -38,9 +38,11 @@
 //     by 8 gives (k4, k5) and (k6, k7) the same way.  v_dot2_f32_f16 on these
 //     (exact products, fp32 sums) yields sum u*x up to a power of two, and
 //     sum q*x = sum u*x - 8 * sum x, with sum x per chunk shared by all rows
-//     of the wave.  5 bit operations and 4 dot2 per 8 weights per x row.
-//   * A DPP wave reduction leaves the totals in lane 63, which rounds to
-//     fp16 (RNE) and stores them.  Rows past N_p are clamped to row N_p - 1
+//     of the wave.  5 bit operations and 4 dot2 per 8 weights per x row; the
+//     accumulators stay scaled by 2^-24 until the final store.
+//   * A DPP wave reduction (both rows of a two-row wave at once, after a
+//     permlane32 swap) leaves the totals in lanes 31 / 63, which round to
+//     fp16 (RNE) and store them.  Rows past N_p are clamped to row N_p - 1
 //     for loading and never stored.
 #include <limits.h>
 #include <stddef.h>
@@ -87,19 +89,26 @@ __device__ __forceinline__ void split_chunk(const u32x4& wv, ChunkNibbles& nb) {
   }
 }
 
-// sum_{k in chunk} q[k] * x[k] for one row and one x row, in fp32.
-__device__ __forceinline__ float chunk_dot(const ChunkNibbles& nb, const u32x4 (&xv)[4], float xsum) {
-  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+// 2^-24 * sum_{k in chunk} q[k] * x[k] for one row and one x row, in fp32, given
+// xs8 = -8 * 2^-24 * sum x.  The dot products of the 2^-24-scaled pairs (k0,k1), (k4,k5)
+// accumulate on top of xs8 and those of the 2^-20-scaled pairs (k2,k3), (k6,k7) separately,
+// so A + B/16 = 2^-24 * (sum u*x - 8 * sum x) with q = u - 8.  The row accumulators stay in
+// this 2^-24 domain (all values far above fp32's normal range limit) and are scaled by 2^24,
+// exactly, before rounding to fp16.
+__device__ __forceinline__ float chunk_dot(const ChunkNibbles& nb, const u32x4 (&xv)[4], float xs8) {
+  float a = xs8, b = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    a0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][0]), bit_cast<half2_t>(xv[j][0]), a0, false);
-    b0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][1]), bit_cast<half2_t>(xv[j][1]), b0, false);
-    a1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][2]), bit_cast<half2_t>(xv[j][2]), a1, false);
-    b1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][3]), bit_cast<half2_t>(xv[j][3]), b1, false);
+    a = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][0]), bit_cast<half2_t>(xv[j][0]), a, false);
+    b = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][1]), bit_cast<half2_t>(xv[j][1]), b, false);
+    a = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][2]), bit_cast<half2_t>(xv[j][2]), a, false);
+    b = __builtin_amdgcn_fdot2(bit_cast<half2_t>(nb.t[j][3]), bit_cast<half2_t>(xv[j][3]), b, false);
   }
-  const float ux = fmaf(b0 + b1, 0.0625f, a0 + a1) * 16777216.0f;  // 2^24 * (A + B / 16) = sum u*x
-  return fmaf(-8.0f, xsum, ux);                                     // q = u - 8
+  return fmaf(b, 0.0625f, a);
 }
+
+constexpr float kTwoPow24 = 16777216.0f;
+constexpr float kMinus8TwoPowMinus24 = -4.76837158203125e-07f;  // -8 * 2^-24
 
 // The workgroup's LDS copy of x (dynamic shared memory, sized per launch; plan.x_lds only).
 extern __shared__ __attribute__((aligned(1024))) u32x4 gemv_x_lds[];
@@ -198,9 +207,9 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
 #pragma unroll
           for (int j = 0; j < 4; ++j) xm[j] = xp[j];
         }
-        const float xsum = chunk_xsum(xm);
+        const float xs8 = chunk_xsum(xm) * kMinus8TwoPowMinus24;
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = fmaf((float)sv[u][r], chunk_dot(nb[r], xm, xsum), acc[m][r]);
+        for (int r = 0; r < R; ++r) acc[m][r] = fmaf((float)sv[u][r], chunk_dot(nb[r], xm, xs8), acc[m][r]);
       }
     }
   }
@@ -262,17 +271,24 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
     }
   }
 
+  // Two rows in one reduction: v_permlane32_swap leaves (row a lanes 0-31, row b lanes 0-31) in
+  // one register and (row a lanes 32-63, row b lanes 32-63) in the other, so their sum holds row
+  // a in lanes 0-31 and row b in lanes 32-63, and lanes 31 and 63 end with the totals.  A
+  // one-row wave pairs its row with itself, which adds in the same order, so a problem gives
+  // the same bits for R = 1 and R = 2.
+  static_assert(R == 1 || R == 2, "rows per wave");
 #pragma unroll
-  for (int m = 0; m < M; ++m)
+  for (int m = 0; m < M; ++m) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][0]), __float_as_uint(acc[m][R - 1]),
+                                                     false, false);
+    acc[m][0] = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+  }
+  if ((lane & 31) == 31 && (R == 2 || lane == 31)) {
+    const int n = row0 + (lane >> 5);
+    if (n < N) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = wave_sum_lane63(acc[m][r]);
-
-  if (lane == 63) {
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (row0 + r < N) y[(size_t)m * N + row0 + r] = (half_t)acc[m][r];
+      for (int m = 0; m < M; ++m) y[(size_t)m * N + n] = (half_t)(acc[m][0] * kTwoPow24);
+    }
   }
 }
 
