@@ -276,18 +276,28 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   // a in lanes 0-31 and row b in lanes 32-63, and lanes 31 and 63 end with the totals.  A
   // one-row wave pairs its row with itself, which adds in the same order, so a problem gives
   // the same bits for R = 1 and R = 2.
-  static_assert(R == 1 || R == 2, "rows per wave");
+  // A third row is reduced on its own, paired with itself, and stored from lane 31.
+  static_assert(R >= 1 && R <= 3, "rows per wave");
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][0]), __float_as_uint(acc[m][R - 1]),
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][0]), __float_as_uint(acc[m][R >= 2 ? 1 : 0]),
                                                      false, false);
     acc[m][0] = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+    if constexpr (R == 3) {
+      const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][2]), __float_as_uint(acc[m][2]), false,
+                                                       false);
+      acc[m][2] = half_sum_lanes31_63(__uint_as_float(s2[0]) + __uint_as_float(s2[1]));
+    }
   }
-  if ((lane & 31) == 31 && (R == 2 || lane == 31)) {
+  if ((lane & 31) == 31 && (R >= 2 || lane == 31)) {
     const int n = row0 + (lane >> 5);
     if (n < N) {
 #pragma unroll
       for (int m = 0; m < M; ++m) y[(size_t)m * N + n] = (half_t)(acc[m][0] * kTwoPow24);
+    }
+    if (R == 3 && lane == 31 && row0 + 2 < N) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) y[(size_t)m * N + row0 + 2] = (half_t)(acc[m][R - 1] * kTwoPow24);
     }
   }
 }
@@ -333,12 +343,25 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(i
                 "slot layout");
   const char* desc = reinterpret_cast<const char*>(&table.slot[p]);
   const u64x4 ptr = *reinterpret_cast<const u64x4*>(desc);  // x, packed, scales, y
-  const i32x4 nkw = *reinterpret_cast<const i32x4*>(desc + 32);  // N, K, wave0, pad
+  const i32x4 nkw = *reinterpret_cast<const i32x4*>(desc + 32);  // N, K, wave0, rows per wave
   typedef const __attribute__((address_space(1))) half_t* gh_t;
   typedef const __attribute__((address_space(1))) uint32_t* gu_t;
   typedef __attribute__((address_space(1))) half_t* gy_t;
-  gemv_rows<M, R, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
-                              (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift, (gwave - nkw.z) * R, lane);
+  if constexpr (R == 3) {
+    // Mixed launch: each problem carries its own rows per wavefront (2 or 3) in the slot.
+    if (nkw.w == 3)
+      gemv_rows<M, 3, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
+                                  (const half_t*)(gh_t)ptr.z, (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift,
+                                  (gwave - nkw.z) * 3, lane);
+    else
+      gemv_rows<M, 2, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
+                                  (const half_t*)(gh_t)ptr.z, (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift,
+                                  (gwave - nkw.z) * 2, lane);
+  } else {
+    gemv_rows<M, R, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
+                                (const half_t*)(gh_t)ptr.z, (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift,
+                                (gwave - nkw.z) * R, lane);
+  }
 }
 
 typedef void (*GemvFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int);
@@ -360,8 +383,23 @@ void* pick_u(int U) {
   }
 }
 
+// Grouped launch with 2 or 3 rows per wavefront per problem (M <= 2 only).
+template <bool XLDS, int M>
+void* pick_mixed(int U) {
+  switch (U) {
+    case 1: return (void*)gemv_grouped_kernel<M, 3, 1, XLDS>;
+    case 2: return (void*)gemv_grouped_kernel<M, 3, 2, XLDS>;
+    case 3: return (void*)gemv_grouped_kernel<M, 3, 3, XLDS>;
+    default: return (void*)gemv_grouped_kernel<M, 3, 4, XLDS>;
+  }
+}
+
 template <bool GROUPED, bool XLDS, int M>
 void* pick_r(int R, int U) {
+  if (R == 3) {
+    if constexpr (GROUPED && M <= 2) return pick_mixed<XLDS, M>(U);
+    return nullptr;  // the plan never asks for it
+  }
   return R == 1 ? pick_u<GROUPED, XLDS, M, 1>(U) : pick_u<GROUPED, XLDS, M, 2>(U);
 }
 
@@ -416,6 +454,31 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   // row; one LDS copy per workgroup removes that traffic (7 TinyLlama linears at M = 1:
   // 6.9 -> 6.3 us on MI355X) wherever x fits the LDS budget.
   p.x_lds = x_lds_bytes(M, max_k) <= (size_t)kGemvMaxLdsX;
+  for (int i = 0; i < count; ++i) p.rows[i] = p.rows_per_wave;
+  // A grouped launch whose two-row wavefronts outnumber the wave slots (8 per SIMD) runs
+  // its last wavefronts in a second round, a full memory round trip after the others.  The
+  // largest problems then take three rows per wavefront, just enough of them for the grid
+  // to fit (7 TinyLlama linears: 8,960 two-row wavefronts for 8,192 slots).
+  if (p.rows_per_wave == 2 && count > 1 && M <= 2) {
+    const long slots = 32L * cus;
+    auto waves_of = [&](int i) {
+      long w = (N[i] + p.rows[i] - 1) / p.rows[i];
+      if (p.x_lds) w = (w + kGemvWavesPerBlock - 1) / kGemvWavesPerBlock * kGemvWavesPerBlock;
+      return w;
+    };
+    long total = 0;
+    for (int i = 0; i < count; ++i) total += waves_of(i);
+    while (total > slots) {
+      int best = -1;
+      for (int i = 0; i < count; ++i)
+        if (p.rows[i] == 2 && (best < 0 || N[i] > N[best])) best = i;
+      if (best < 0) break;
+      total -= waves_of(best);
+      p.rows[best] = 3;
+      total += waves_of(best);
+      p.rows_per_wave = 3;  // mixed launch
+    }
+  }
   return p;
 }
 
@@ -447,8 +510,9 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
   for (int i = 0; i < kMaxGemvGroup; ++i) {
     if (i < count) {
       const GemvProblem& q = problems[order[i]];
-      table.slot[i] = GemvSlot{q.x, q.packed, q.scales, q.y, q.N, q.K, waves, 0};
-      int w = ceil_div(q.N, plan.rows_per_wave);
+      const int rows = plan.rows[order[i]];
+      table.slot[i] = GemvSlot{q.x, q.packed, q.scales, q.y, q.N, q.K, waves, rows};
+      int w = ceil_div(q.N, rows);
       if (plan.x_lds) w = ceil_div(w, kGemvWavesPerBlock) * kGemvWavesPerBlock;  // whole workgroups
       waves += w;
       bounds[i] = waves;

@@ -32,7 +32,7 @@ struct GemvSlot {
   int N;
   int K;
   int wave0;
-  int pad;
+  int rows;  // rows per wavefront of this problem
 };
 
 // The grouped kernel's arguments: the lookup header as ten scalar arguments (preloaded into
@@ -49,9 +49,10 @@ constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
 constexpr int kGemvMaxLdsX = 20480;
 
 struct GemvPlan {
-  int rows_per_wave;   // R: output rows one wavefront owns
+  int rows_per_wave;   // R: output rows one wavefront owns (3: grouped launch mixing 2 and 3)
   int unroll;          // U: 64-chunk blocks (64 lanes x 32 k) whose loads one pass keeps in flight
   bool x_lds;          // each workgroup copies x into LDS once (else every lane loads its x)
+  int rows[kMaxGemvGroup];  // rows per wavefront of each problem (in the caller's order)
 };
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
