@@ -551,7 +551,7 @@ def main() -> int:
                      "frac": round(achieved / SPEC_HBM_GBPS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,
                      "traffic_detail": traffic,
-                     "kernel": "kf::gemv_grouped_kernel<1,2,1,x in LDS> (7 TinyLlama linears)",
+                     "kernel": "kf::gemv_grouped_kernel<1,3,1,x in LDS> (7 TinyLlama linears; gate at 3 rows per wavefront)",
                      "bytes_per_launch": step_bytes, "avg_launch_us": round(gemv_avg_ms * 1e3, 3),
                      "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4),
                      "frac_of_measured_read": round(achieved / ceil["hbm_read_gbps"], 4)},
