@@ -31,7 +31,9 @@ Protocol
   stream; achieved = 22,779,904 B / that duration.
 * ceilings: HBM copy/read peaks measured in the same run with the library's
   dwordx4 kernels on 1 GiB buffers; fp16 MFMA peak with torch.matmul
-  (hipBLASLt) at 4096/6144/8192.
+  (hipBLASLt) at 4096/6144/8192.  Also the bare read of exactly one step's
+  bytes in one launch (same rotation and graph protocol): the ceiling a
+  one-launch step of this size can reach, launch and ramp included.
 * M=2048 (BASELINE config 4's largest point): the MFMA GEMM on every
   TinyLlama shape, 10 launches per HIP graph, HIP events around replays;
   TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum, each beside
@@ -315,6 +317,31 @@ def measure_hbm(torch, lib, kl) -> dict:
     return {"hbm_copy_gbps": best["copy"], "hbm_read_gbps": best["read"], "buffer_bytes": nbytes}
 
 
+def measure_same_size_read(torch, lib, kl, nbytes: int, copies: int = 24) -> dict:
+    """The bare-read ceiling for one step: kf_bw_read over exactly `nbytes` in one launch, from
+    `copies` disjoint windows rotated so every launch reads from HBM, graph-replayed like the
+    step itself.  Best over grid sizes (one 16-byte load per thread, and grid-stride loops)."""
+    nbytes = nbytes // 16 * 16
+    buf = torch.empty(copies * nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    one_shot = -(-nbytes // (16 * 256))
+    best = None
+    for grid in sorted({min(one_shot, 1 << 16), 8 * cus, 16 * cus}):
+        def step(r, grid=grid):
+            kl.check(lib.kf_bw_read(buf.data_ptr() + r * nbytes, sink.data_ptr(), nbytes, grid,
+                                    torch.cuda.current_stream().cuda_stream), "read")
+        steps = GraphSteps(torch, step, copies)
+        us = statistics.median(steps.event_avg_ms(4 * copies) for _ in range(5)) * 1e3
+        if best is None or us < best["us"]:
+            best = {"us": round(us, 3), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "grid_blocks": grid,
+                    "bytes": nbytes}
+        del steps
+    del buf, sink
+    torch.cuda.empty_cache()
+    return best
+
+
 def measure_mfma_peak(torch) -> float:
     best = 0.0
     for s in (4096, 6144, 8192):
@@ -377,6 +404,8 @@ def main() -> int:
     names = [ly["name"] for ly in layers]
     idx = {nm: i for i, nm in enumerate(names)}
     step_bytes = sum(algo_bytes(1, ly["N"], ly["K"]) for ly in layers)
+    same_read = measure_same_size_read(torch, lib, kl, step_bytes)
+    log(f"bare read of one step's {step_bytes} B in one launch: {same_read['us']} us = {same_read['gbps']} GB/s")
     set_bytes = sum(ly["packed"].numel() * 4 + ly["scales"].numel() * 2 for ly in layers)
     copies = max(2, -(-(2 * MALL_BYTES) // set_bytes))
     dev = [[(ly["packed"].cuda(), ly["scales"].cuda()) for ly in layers] for _ in range(copies)]
@@ -568,7 +597,9 @@ def main() -> int:
                      "kernel": "kf::gemv_grouped_kernel<1,3,1,x in LDS> (7 TinyLlama linears; gate at 3 rows per wavefront)",
                      "bytes_per_launch": step_bytes, "avg_launch_us": round(gemv_avg_ms * 1e3, 3),
                      "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4),
-                     "frac_of_measured_read": round(achieved / ceil["hbm_read_gbps"], 4)},
+                     "frac_of_measured_read": round(achieved / ceil["hbm_read_gbps"], 4),
+                     "same_size_read": same_read,
+                     "frac_of_same_size_read": round(achieved / same_read["gbps"], 4)},
         "cpu_baseline": cpu,
         "ceilings": {k: round(v, 1) if isinstance(v, float) else v for k, v in ceil.items()},
         "step_structures": structures,
