@@ -24,10 +24,12 @@ from kernelforge import _lib
 # (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
 # skinny MFMA kernel for small M, then the tiled MFMA kernels.
 GEMV_MAX_M = 2
-# The GEMV accepts every N for M <= 8 (as the reference's does); the MFMA kernels need
-# N % 64 == 0.  Between GEMV_MAX_M and this bound a shape the GEMM cannot take stays on
-# the GEMV, so int4_matmul accepts exactly what the reference's accepts.
-_GEMV_LIMIT_M = 8
+# The reference's int4_matmul sends M <= 7 to its GEMV, which accepts every N, and M >= 8
+# to its GEMM, which rejects N % 64 != 0 (kernelforge/ops.py:193,204-214).  Our MFMA kernels
+# need N % 64 == 0 as well, so between GEMV_MAX_M and 7 a shape the GEMM cannot take stays
+# on the GEMV: int4_matmul accepts exactly what the reference's accepts and raises the same
+# ValueError for the rest.
+_GEMV_LIMIT_M = 7
 
 
 def _use_gemv(m: int, n: int) -> bool:
@@ -213,8 +215,8 @@ def gemm_plan(m: int, n: int, k: int, group_size: int = 128, device: torch.devic
 def int4_matmul(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """y = x @ W_hat^T for INT4 weights from kernelforge.quantize, choosing the kernel by M.
 
-    M <= GEMV_MAX_M: the bandwidth-bound GEMV; larger M: the MFMA GEMM (M <= 8 with N not
-    a multiple of 64 stays on the GEMV).  Reference kernelforge/ops.py:204-214.
+    M <= GEMV_MAX_M: the bandwidth-bound GEMV; larger M: the MFMA GEMM (M <= 7 with N not
+    a multiple of 64 stays on the GEMV, as in the reference).  Reference kernelforge/ops.py:204-214.
     """
     if _use_gemv(x.shape[0], packed.shape[0]):
         return int4_gemv(x, packed, scales, group_size)

@@ -236,6 +236,18 @@ def test_matmul_dispatcher(error_log, m):
     _check(error_log, "int4_matmul", ops.int4_matmul, m, 2048, 2048, 128, "dispatch")
 
 
+def test_matmul_ragged_n_follows_the_reference_dispatch():
+    """Reference int4_matmul (kernelforge/ops.py:193,212): M <= 7 -> GEMV (any N), M >= 8 -> GEMM,
+    which rejects N % 64 != 0."""
+    packed, scales, dp, ds = _weights(100, 256, 128)
+    x7 = _x(7, 256, 7)
+    y = ops.int4_matmul(torch.from_numpy(x7).to(DEV), dp, ds, 128)
+    torch.cuda.synchronize()
+    assert o.max_rel_err(y.float().cpu().numpy(), o.linear_ref_fp32(x7, packed, scales, 128)) <= REL_TOL
+    with pytest.raises(ValueError, match="multiple of 64"):
+        ops.int4_matmul(torch.from_numpy(_x(8, 256, 8)).to(DEV), dp, ds, 128)
+
+
 def test_gemm_rejects_n_not_multiple_of_64():
     _, _, dp, ds = _weights(100, 256, 128)
     x = torch.randn(16, 256, device=DEV).half()
