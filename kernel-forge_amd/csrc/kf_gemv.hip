@@ -24,9 +24,10 @@
 //     than the weights do.  When M*K fp16 values fit 20 KiB, each workgroup
 //     copies x into LDS once with LDS-DMA (issued before the weight loads) and
 //     the lanes read their x from there; otherwise every lane loads its own.
-//   * Each wavefront owns R consecutive rows of one problem.  Lane l handles
-//     chunks l, l+64, ... of its rows, so a wavefront-wide dwordx4 streams
-//     1 KiB of a row contiguously.
+//   * Each wavefront owns R consecutive rows of one problem (R = 1 or 2; a
+//     grouped launch that would not fit one resident round gives its largest
+//     problems 3).  Lane l handles chunks l, l+64, ... of its rows, so a
+//     wavefront-wide dwordx4 streams 1 KiB of a row contiguously.
 //   * A pass covers UU (1..4) consecutive 64-chunk blocks; UU is picked per
 //     pass from the chunks left in the row, so a K=5632 row is one pass of
 //     3 blocks and a K=2048 row one pass of 1, in the same launch.  Every load
@@ -280,8 +281,8 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   static_assert(R >= 1 && R <= 3, "rows per wave");
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][0]), __float_as_uint(acc[m][R >= 2 ? 1 : 0]),
-                                                     false, false);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][0]),
+                                                     __float_as_uint(acc[m][R >= 2 ? 1 : 0]), false, false);
     acc[m][0] = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
     if constexpr (R == 3) {
       const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[m][2]), __float_as_uint(acc[m][2]), false,
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(i
   typedef const __attribute__((address_space(1))) half_t* gh_t;
   typedef const __attribute__((address_space(1))) uint32_t* gu_t;
   typedef __attribute__((address_space(1))) half_t* gy_t;
-  if constexpr (R == 3) {
+  if constexpr (R == kGemvRowsMixed) {
     // Mixed launch: each problem carries its own rows per wavefront (2 or 3) in the slot.
     if (nkw.w == 3)
       gemv_rows<M, 3, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
@@ -386,17 +387,18 @@ void* pick_u(int U) {
 // Grouped launch with 2 or 3 rows per wavefront per problem (M <= 2 only).
 template <bool XLDS, int M>
 void* pick_mixed(int U) {
+  constexpr int RM = kGemvRowsMixed;
   switch (U) {
-    case 1: return (void*)gemv_grouped_kernel<M, 3, 1, XLDS>;
-    case 2: return (void*)gemv_grouped_kernel<M, 3, 2, XLDS>;
-    case 3: return (void*)gemv_grouped_kernel<M, 3, 3, XLDS>;
-    default: return (void*)gemv_grouped_kernel<M, 3, 4, XLDS>;
+    case 1: return (void*)gemv_grouped_kernel<M, RM, 1, XLDS>;
+    case 2: return (void*)gemv_grouped_kernel<M, RM, 2, XLDS>;
+    case 3: return (void*)gemv_grouped_kernel<M, RM, 3, XLDS>;
+    default: return (void*)gemv_grouped_kernel<M, RM, 4, XLDS>;
   }
 }
 
 template <bool GROUPED, bool XLDS, int M>
 void* pick_r(int R, int U) {
-  if (R == 3) {
+  if (R == kGemvRowsMixed) {
     if constexpr (GROUPED && M <= 2) return pick_mixed<XLDS, M>(U);
     return nullptr;  // the plan never asks for it
   }
@@ -476,7 +478,7 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
       total -= waves_of(best);
       p.rows[best] = 3;
       total += waves_of(best);
-      p.rows_per_wave = 3;  // mixed launch
+      p.rows_per_wave = kGemvRowsMixed;
     }
   }
   return p;

@@ -48,8 +48,12 @@ constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
 // workgroups (32 wavefronts) per CU within the 160 KiB of LDS.
 constexpr int kGemvMaxLdsX = 20480;
 
+// GemvPlan::rows_per_wave of a grouped launch whose problems take 2 or 3 rows per wavefront
+// each (GemvPlan::rows, GemvSlot::rows); also the grouped kernel's template rows for it.
+constexpr int kGemvRowsMixed = 3;
+
 struct GemvPlan {
-  int rows_per_wave;   // R: output rows one wavefront owns (3: grouped launch mixing 2 and 3)
+  int rows_per_wave;   // R: output rows one wavefront owns, or kGemvRowsMixed
   int unroll;          // U: 64-chunk blocks (64 lanes x 32 k) whose loads one pass keeps in flight
   bool x_lds;          // each workgroup copies x into LDS once (else every lane loads its x)
   int rows[kMaxGemvGroup];  // rows per wavefront of each problem (in the caller's order)
