@@ -373,6 +373,37 @@ def test_output_guard_bands(kind, m, n, k):
     assert o.max_rel_err(y, o.linear_ref_fp32(_x(m, k, 5), packed, scales, g)) <= REL_TOL
 
 
+@pytest.mark.parametrize("m", [1, 2])
+def test_grouped_guard_bands_three_row_waves(m):
+    """A grouped launch too large for one resident round at two rows per wavefront (> 8 per SIMD),
+    so its largest problems take three rows: ragged N (not a multiple of 3), every output inside
+    its guard bands, bit-identical to its own single launch, within tolerance of the oracle."""
+    g, k = 128, 1024
+    ns = [9001, 8999, 4099, 257, 3, 1]
+    guard = 2048
+    sentinel = torch.tensor(-12345.0, dtype=torch.float16)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    cases, bufs = [], []
+    probs = (_lib.GemvProblem * len(ns))()
+    for i, n in enumerate(ns):
+        packed, scales, dp, ds = _weights(n, k, g)
+        xh = _x(m, k, 300 + i)
+        x = torch.from_numpy(xh).to(DEV)
+        buf = torch.full((guard + m * n + guard,), float(sentinel), dtype=torch.float16, device=DEV)
+        probs[i] = _lib.GemvProblem(x.data_ptr(), dp.data_ptr(), ds.data_ptr(), buf.data_ptr() + 2 * guard, n, k)
+        cases.append((n, xh, x, packed, scales, dp, ds))
+        bufs.append(buf)
+    _lib.check(lib.kf_int4_gemv_grouped(probs, len(ns), m, g, stream), "int4_gemv_grouped")
+    for (n, xh, x, packed, scales, dp, ds), buf in zip(cases, bufs):
+        host = buf.cpu()
+        assert (host[:guard] == sentinel).all() and (host[guard + m * n:] == sentinel).all(), f"N={n}: write outside y"
+        y = host[guard:guard + m * n].reshape(m, n)
+        assert not (y == sentinel).any(), f"N={n}: unwritten output element"
+        assert torch.equal(y.to(DEV), ops.int4_gemv(x, dp, ds, g)), f"N={n}: grouped differs from single"
+        assert o.max_rel_err(y.float().numpy(), o.linear_ref_fp32(xh, packed, scales, g)) <= REL_TOL
+
+
 # ---------------------------------------------------------------------------
 # int4_linear, modules, graph capture
 # ---------------------------------------------------------------------------
