@@ -186,6 +186,19 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of the math
+  // With x in LDS, the chunk sums of x need nothing from the weight loads: computed here, ahead
+  // of the first weight use, they run while those loads are in flight instead of after the
+  // wait for them (same operations in the same order, so the same bits).  M <= 2 only: above
+  // that the extra live sums cost occupancy in the unrolled kernels.
+  constexpr bool kEarlyXsum = XLDS && M <= 2;
+  float xs8_early[UU][XM];
+  if constexpr (kEarlyXsum) {
+#pragma unroll
+    for (int u = 0; u < UU; ++u)
+#pragma unroll
+      for (int m = 0; m < XM; ++m) xs8_early[u][m] = chunk_xsum(xv[u][m]) * kMinus8TwoPowMinus24;
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int u = 0; u < UU; ++u) {
     const int c = cb + lane + 64 * u;
@@ -208,7 +221,7 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
 #pragma unroll
           for (int j = 0; j < 4; ++j) xm[j] = xp[j];
         }
-        const float xs8 = chunk_xsum(xm) * kMinus8TwoPowMinus24;
+        const float xs8 = kEarlyXsum && m < XM ? xs8_early[u][m < XM ? m : 0] : chunk_xsum(xm) * kMinus8TwoPowMinus24;
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = fmaf((float)sv[u][r], chunk_dot(nb[r], xm, xs8), acc[m][r]);
       }
