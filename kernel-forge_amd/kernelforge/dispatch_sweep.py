@@ -5,8 +5,10 @@ For every layer shape and M it times ``ops.int4_gemv`` (M <= 8) and ``ops.int4_g
 events around graph replays of back-to-back launches (weights rotated so each launch reads them
 from HBM), and applies the reference's rule (bench/sweep_int4_dispatch.py:51-57): GEMV_MAX_M is
 the largest M at which the sum of GEMV times over the shapes is below the sum of GEMM times.
+With ``--fp16`` it also times ``F.linear`` on fp16 weights of the same shape (hipBLASLt), the
+baseline the reference's bench/bench_gemm.py:83 calls ``cublas_fp16``.
 
-    python kernel-forge_amd/kernelforge/dispatch_sweep.py [--out sweep.json] [--ms 1,2,4,8,16]
+    python kernel-forge_amd/kernelforge/dispatch_sweep.py [--out sweep.json] [--ms 1,2,4,8,16] [--fp16]
 """
 
 from __future__ import annotations
@@ -56,12 +58,17 @@ def time_us(fn_for_copy, copies: int, reps: int = 3) -> float:
     return s.elapsed_time(e) * 1e3 / (reps * copies)
 
 
-def sweep(ms: list[int], shapes: dict, group: int = 128) -> dict:
+def sweep(ms: list[int], shapes: dict, group: int = 128, fp16: bool = False) -> dict:
     res = {}
     for name, (n, k) in shapes.items():
-        qw = kq.quantize_weight(torch.randn(n, k, generator=torch.Generator().manual_seed(n + k)) * 0.02, group)
+        w = torch.randn(n, k, generator=torch.Generator().manual_seed(n + k)) * 0.02
+        qw = kq.quantize_weight(w, group)
         copies = max(2, min(32, -(-(2 * MALL_BYTES) // qw.nbytes)))
         dev = [(qw.packed.cuda(), qw.scales.cuda()) for _ in range(copies)]
+        w16 = []
+        if fp16:
+            copies16 = max(2, min(32, -(-(2 * MALL_BYTES) // (2 * n * k))))
+            w16 = [w.half().cuda() for _ in range(copies16)]
         res[name] = {}
         for m in ms:
             x = torch.randn(m, k, device="cuda").half()
@@ -73,10 +80,14 @@ def sweep(ms: list[int], shapes: dict, group: int = 128) -> dict:
                 plan = ops.gemm_plan(m, n, k, group)
                 row["gemm_kernel"] = f"{plan['kernel']}/{plan['splits']}"  # tile-table index (or skinny) / splits
             row["tflops_best"] = 2 * m * n * k / min(v for kk, v in row.items() if kk.endswith("_us")) / 1e6
+            if w16:
+                row["fp16_us"] = time_us(lambda c: torch.nn.functional.linear(x, w16[c]), len(w16))
+                int4_us = min(v for kk, v in row.items() if kk in ("gemv_us", "gemm_us"))
+                row["fp16_over_int4"] = row["fp16_us"] / int4_us
             res[name][m] = row
             print(f"{name} M={m}: " + " ".join(f"{kk}={v:.2f}" if isinstance(v, float) else f"{kk}={v}"
                                               for kk, v in row.items()), flush=True)
-        del dev
+        del dev, w16
         torch.cuda.empty_cache()
     return res
 
@@ -99,10 +110,11 @@ def main() -> None:
     ap.add_argument("--ms", default="1,2,3,4,5,6,7,8,9,16,32,64,128,256,512,2048")
     ap.add_argument("--shapes", default=",".join(SHAPES))
     ap.add_argument("--out", default=None)
+    ap.add_argument("--fp16", action="store_true", help="also time F.linear on fp16 weights (hipBLASLt)")
     args = ap.parse_args()
     ms = [int(v) for v in args.ms.split(",")]
     shapes = {s: SHAPES[s] for s in args.shapes.split(",")}
-    res = sweep(ms, shapes)
+    res = sweep(ms, shapes, fp16=args.fp16)
     out = {"results_us": res, "gemv_max_m": crossover(res, ms), "current_GEMV_MAX_M": ops.GEMV_MAX_M,
            "device": torch.cuda.get_device_name(0)}
     print(json.dumps({"gemv_max_m": out["gemv_max_m"]}), flush=True)
