@@ -47,7 +47,12 @@ int kf_abi_version(void);
  * TORCH_CHECK in csrc/gemm/dequant_gemv.cu:5-19). */
 const char* kf_last_error(void);
 
-/* Fused dequant GEMV for M in [1, 8], any N >= 1, K % G == 0, G in {64, 128}.
+/* Largest N one launch accepts (for a grouped GEMV: the sum of N over its
+ * problems).  At one row per wavefront this keeps a launch below 2^31
+ * work-items; larger N returns KF_ERR_UNSUPPORTED.  No reference counterpart. */
+#define KF_MAX_ROWS ((1 << 25) - 64)
+
+/* Fused dequant GEMV for M in [1, 8], N in [1, KF_MAX_ROWS], K % G == 0, G in {64, 128}.
  * x and packed must be 16-byte aligned.
  * Replaces kf::gemv::dispatch (csrc/gemm/dequant_gemv_kernel.cuh:120-142)
  * and the pybind entry _C.int4_gemv (csrc/bindings.cpp:24-25,
@@ -93,7 +98,7 @@ size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size);
 int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num_kernels,
                       int* splits, int* block_m, int* block_n);
 
-/* MFMA dequant GEMM, any M >= 1, N % 64 == 0, K % G == 0, G in {64, 128}.
+/* MFMA dequant GEMM, any M >= 1, N % 64 == 0 and N <= KF_MAX_ROWS, K % G == 0, G in {64, 128}.
  * ws may be NULL when kf_int4_gemm_workspace_bytes() returned 0.
  * Replaces kf::gemm_tc::run (dequant_gemm_tc_kernel.cuh:203-211) and the
  * pybind entry _C.int4_gemm (csrc/bindings.cpp:26-27,

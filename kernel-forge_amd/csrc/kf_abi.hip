@@ -66,6 +66,7 @@ int check_common(const void* x, const void* packed, const void* scales, const vo
                  int group_size) {
   if (!x || !packed || !scales || !y) return fail(KF_ERR_INVALID_ARG, "x, packed, scales and y must be non-null");
   if (M < 1 || N < 1 || K < 1) return fail(KF_ERR_INVALID_ARG, "M, N, K must be positive, got M=%d N=%d K=%d", M, N, K);
+  if (N > KF_MAX_ROWS) return fail(KF_ERR_UNSUPPORTED, "N=%d exceeds the %d rows one launch supports", N, KF_MAX_ROWS);
   if (group_size != 64 && group_size != 128)
     return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);
   if (K % group_size != 0)
@@ -131,7 +132,7 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
   if (M < 1 || M > 8) return fail(KF_ERR_INVALID_ARG, "int4_gemv handles M in [1, 8], got M=%d", M);
   kf::GemvProblem probs[KF_GEMV_MAX_GROUP];
   int ns[KF_GEMV_MAX_GROUP], ks[KF_GEMV_MAX_GROUP];
-  long waves = 0;
+  long rows = 0;
   for (int i = 0; i < count; ++i) {
     const kf_gemv_problem& p = problems[i];
     int st = check_common(p.x, p.packed, p.scales, p.y, M, p.N, p.K, group_size);
@@ -139,9 +140,11 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
     probs[i] = {p.x, p.packed, p.scales, p.y, p.N, p.K};
     ns[i] = p.N;
     ks[i] = p.K;
-    waves += p.N;
+    rows += p.N;
   }
-  if (waves > (1L << 30)) return fail(KF_ERR_UNSUPPORTED, "total rows %ld too large for one launch", waves);
+  if (rows > KF_MAX_ROWS)
+    return fail(KF_ERR_UNSUPPORTED, "the problems have %ld rows in total, more than the %d one launch supports", rows,
+                KF_MAX_ROWS);
   int cus = 0;
   int st = cu_count(&cus);
   if (st) return st;

@@ -12,6 +12,11 @@ import pytest
 from kernelforge import _lib
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "kf_int4.h"
+MAX_ROWS = (1 << 25) - 64  # KF_MAX_ROWS in the header
+
+
+def test_row_limit_matches_header():
+    assert re.search(r"#define KF_MAX_ROWS \(\(1 << 25\) - 64\)", HEADER.read_text())
 
 
 def _declared_symbols() -> set[str]:
@@ -60,6 +65,20 @@ def test_grouped_gemv_argument_errors_without_gpu():
     _err(lib.kf_int4_gemv_grouped(arr, 2, 9, 128, None), r"M in \[1, 8\]")
     mixed = (_lib.GemvProblem * 2)(good, bad_k)
     _err(lib.kf_int4_gemv_grouped(mixed, 2, 1, 128, None), "problem 1: K=200 is not a multiple of group_size")
+    half = _lib.GemvProblem(0x1000, 0x1000, 0x1000, 0x1000, MAX_ROWS // 2 + 64, 256)
+    _err(lib.kf_int4_gemv_grouped((_lib.GemvProblem * 2)(half, half), 2, 1, 128, None),
+         f"rows in total, more than the {MAX_ROWS}")
+
+
+def test_row_limit_without_gpu():
+    """N beyond KF_MAX_ROWS (a grid past 2^31 work-items at one row per wavefront) is refused
+    before any launch, by the GEMV and the GEMM alike."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    _err(lib.kf_int4_gemv(p, p, p, p, 1, MAX_ROWS + 1, 256, 128, None), f"exceeds the {MAX_ROWS} rows")
+    _err(lib.kf_int4_gemm(p, p, p, p, None, 0, 16, MAX_ROWS + 64, 256, 128, None), f"exceeds the {MAX_ROWS} rows")
+    with pytest.raises(ValueError, match="exceeds"):
+        _lib.check(lib.kf_int4_gemv(p, p, p, p, 1, MAX_ROWS + 1, 256, 128, None), "int4_gemv")
 
 
 def test_gemm_argument_errors_without_gpu():
