@@ -146,8 +146,15 @@ def prepare_mfma16(packed: torch.Tensor, scales: torch.Tensor, group_size: int =
     int4_gemm builds it by itself on first use, except for tensors created under
     torch.inference_mode() (no version counter to notice in-place updates): for those this is
     the only way, and the caller promises not to modify packed / scales in place afterwards.
+    Not during HIP-graph capture.  The host waits for the copy to be written before it is
+    attached, so a later int4_gemm on any stream reads a complete copy.
     """
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("prepare_mfma16 launches a kernel and allocates; call it outside HIP-graph capture")
     packed_r, scales_r = int4_reorder_mfma16(packed, scales, group_size)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(packed.device))
+    done.synchronize()
     setattr(packed, _MFMA16_ATTR, (_mfma16_key(packed, scales, group_size), packed_r, scales_r))
 
 
