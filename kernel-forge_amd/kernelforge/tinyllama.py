@@ -53,22 +53,25 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return (xf * self.weight.float()).to(x.dtype)
+        # One fused kernel when x and the weight share a dtype (fp32 accumulation inside).
+        return torch.nn.functional.rms_norm(x, (x.shape[-1],), self.weight.to(x.dtype), self.eps)
 
 
 def _rope_tables(cfg: TinyLlamaConfig, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """RoPE tables [max_seq, head_dim]: cos, and sin with the sign of rotate-half folded in
+    (-sin on the first half), so x * cos + swap_halves(x) * sin is the rotation."""
     inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32) / cfg.head_dim))
     t = torch.arange(cfg.max_seq, dtype=torch.float32)
     freqs = torch.outer(t, inv)
     emb = torch.cat([freqs, freqs], dim=-1)
-    return emb.cos().to(device), emb.sin().to(device)
+    sin = freqs.sin()
+    return emb.cos().to(device), torch.cat([-sin, sin], dim=-1).to(device)
 
 
-def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+def _rope(x: torch.Tensor, cos: torch.Tensor, sin_signed: torch.Tensor) -> torch.Tensor:
+    """x [T, heads, d] rotated by the per-position rows cos / sin_signed [T, 1, d]."""
     h = x.shape[-1] // 2
-    return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+    return torch.addcmul(x * cos, torch.cat([x[..., h:], x[..., :h]], dim=-1), sin_signed)
 
 
 class FusedInt4Linear(nn.Module):
@@ -92,8 +95,11 @@ class FusedInt4Linear(nn.Module):
         self.register_buffer("scales", torch.cat([p.scales for p in parts], dim=0).contiguous())
 
     def forward(self, x: torch.Tensor) -> list[torch.Tensor]:
-        y = ops.int4_linear(x, self.packed, self.scales, self.group_size)
-        return list(torch.split(y, self.splits, dim=-1))
+        return list(torch.split(self.forward_concat(x), self.splits, dim=-1))
+
+    def forward_concat(self, x: torch.Tensor) -> torch.Tensor:
+        """The parts' outputs side by side along the last dimension (one tensor)."""
+        return ops.int4_linear(x, self.packed, self.scales, self.group_size)
 
 
 class Attention(nn.Module):
@@ -108,29 +114,30 @@ class Attention(nn.Module):
         self.qkv: FusedInt4Linear | None = None
 
     def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
-        """x [1, T, H]; pos int64 [T] positions; cache_* [kv_heads, max_seq, d]; mask [T, max_seq]."""
+        """x [1, T, H]; pos int64 [T] positions; cos / sin [T, 1, d] RoPE rows of those positions
+        (sin with the rotate-half sign folded in); cache_k / cache_v [kv_heads, max_seq, d] slabs,
+        the key slab holding K transposed ([kv_heads, d, max_seq]); mask [rep * T, max_seq], the
+        additive causal mask repeated for the rep = heads / kv_heads query heads of a KV head."""
         cfg = self.cfg
         t = x.shape[1]
+        hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        rep = hq // hkv
         if self.qkv is not None:
-            q, k, v = self.qkv(x)
+            y = self.qkv.forward_concat(x)                               # [1, T, (hq + 2 hkv) d]
+            qk, v = y[..., :(hq + hkv) * d], y[..., (hq + hkv) * d:]
         else:
-            q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
-        q = q.view(t, cfg.heads, cfg.head_dim).transpose(0, 1)        # [Hq, T, d]
-        k = k.view(t, cfg.kv_heads, cfg.head_dim).transpose(0, 1)     # [Hkv, T, d]
-        v = v.view(t, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
-        c, s = cos[pos].to(q.dtype), sin[pos].to(q.dtype)              # [T, d]
-        q = q * c + _rotate_half(q) * s
-        k = k * c + _rotate_half(k) * s
-        cache_k.index_copy_(1, pos, k)
-        cache_v.index_copy_(1, pos, v)
-        rep = cfg.heads // cfg.kv_heads
-        kk = cache_k.repeat_interleave(rep, dim=0)                     # [Hq, S, d]
-        vv = cache_v.repeat_interleave(rep, dim=0)
-        scores = torch.bmm(q.contiguous(), kk.transpose(1, 2).contiguous()).float() / math.sqrt(cfg.head_dim)
-        scores = scores + mask                                         # [Hq, T, S]
-        probs = torch.softmax(scores, dim=-1).to(q.dtype)
-        out = torch.bmm(probs, vv.contiguous())                        # [Hq, T, d]
-        out = out.transpose(0, 1).reshape(1, t, cfg.heads * cfg.head_dim)
+            qk, v = torch.cat([self.q_proj(x), self.k_proj(x)], dim=-1), self.v_proj(x)
+        qk = _rope(qk.view(t, hq + hkv, d), cos, sin)                     # q and k heads together
+        q, k = qk[:, :hq], qk[:, hq:]
+        cache_k.view(hkv, d, cfg.max_seq).index_copy_(2, pos, k.permute(1, 2, 0))
+        cache_v.index_copy_(1, pos, v.view(t, hkv, d).transpose(0, 1))
+        # Query head h reads KV head h // rep: the rep heads of a KV head (and their T positions)
+        # form the rows of one batch entry, so K and V are never repeated.
+        qg = q.reshape(t, hkv, rep, d).permute(1, 2, 0, 3).reshape(hkv, rep * t, d)
+        scores = torch.baddbmm(mask, qg, cache_k.view(hkv, d, cfg.max_seq), alpha=1.0 / math.sqrt(d))
+        probs = torch.softmax(scores, dim=-1)                            # fp32 inside
+        out = torch.bmm(probs, cache_v)                                  # [hkv, rep * T, d]
+        out = out.view(hkv, rep, t, d).permute(2, 0, 1, 3).reshape(1, t, hq * d)
         return self.o_proj(out)
 
 
@@ -186,6 +193,8 @@ class TinyLlama(nn.Module):
 
 
     def new_cache(self, device, dtype=torch.float16) -> torch.Tensor:
+        """KV cache [layers, 2, kv_heads, max_seq, head_dim]; each layer's key slab holds K
+        transposed (read as [kv_heads, head_dim, max_seq]), the value slab V as laid out."""
         c = self.cfg
         return torch.zeros(c.layers, 2, c.kv_heads, c.max_seq, c.head_dim, device=device, dtype=dtype)
 
@@ -195,8 +204,12 @@ class TinyLlama(nn.Module):
         Inference only (no autograd)."""
         cos, sin = rope
         x = self.embed_tokens(tokens).unsqueeze(0)
+        # Per-token inputs shared by every layer: RoPE rows of the positions, and the mask
+        # repeated for the query heads that share a KV head.
+        c, s = cos[pos].to(x.dtype).unsqueeze(1), sin[pos].to(x.dtype).unsqueeze(1)
+        mask_g = mask.to(x.dtype).repeat(self.cfg.heads // self.cfg.kv_heads, 1)
         for i, layer in enumerate(self.layers):
-            x = layer(x, pos, cos, sin, cache[i, 0], cache[i, 1], mask)
+            x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], mask_g)
         x = self.norm(x[:, -1:])
         return self.lm_head(x).float().view(-1)
 
