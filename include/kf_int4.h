@@ -84,6 +84,23 @@ typedef struct kf_gemv_problem {
  * the time to stream a whole small layer. */
 int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int group_size, void* stream);
 
+#define KF_PROLOGUE_NONE 0     /* x as given */
+#define KF_PROLOGUE_RMSNORM 1  /* x * rsqrt(mean(x^2) + eps) * aux, aux = fp16 norm weight [K] */
+#define KF_PROLOGUE_SWIGLU 2   /* fp16(fp16(silu(x)) * aux): x = gate [K], aux = up [K] */
+#define KF_GEMV_FUSED_MAX_K 10240
+
+/* Decode GEMV (M = 1, K <= KF_GEMV_FUSED_MAX_K) with the work either side of a decoder linear
+ * fused in: a prologue transforms x before the product (RMSNorm with weight aux and eps, or
+ * SwiGLU of gate x and up aux, computed on the workgroup's LDS copy of x), and a non-NULL
+ * residual (fp16 [N], may equal y) is added to the fp16 result:
+ * y = fp16(residual + fp16(prologue(x) @ W_hat^T)).  The product is kf_int4_gemv's, bit for bit;
+ * with the residual the output equals torch's residual + int4_linear(x) bit for bit, and the
+ * SwiGLU prologue rounds like torch's silu(gate) * up on fp16 tensors.  aux must be 16-byte
+ * aligned.  No reference counterpart: it fuses the RMSNorm, SiLU-multiply and residual adds
+ * that surround the reference's int4_linear in a decoder layer into the GEMV launch. */
+int kf_int4_gemv_fused(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
+                       int group_size, int prologue, const void* aux, float eps, const void* residual, void* stream);
+
 /* Bytes of fp32 split-K workspace kf_int4_gemm needs for this problem on the
  * current device (0 when the chosen plan has no split-K).
  * Replaces kf::gemm_tc::workspace_floats (dequant_gemm_tc_kernel.cuh:179-183),

@@ -19,6 +19,10 @@
 static_assert(KF_DTYPE_F32 == kf::kQuantF32 && KF_DTYPE_F16 == kf::kQuantF16 && KF_DTYPE_BF16 == kf::kQuantBF16,
               "dtype codes of the C ABI and the kernels differ");
 static_assert(KF_GEMV_MAX_GROUP == kf::kMaxGemvGroup, "header and kernels disagree on the group limit");
+static_assert(KF_PROLOGUE_NONE == kf::kGemvProNone && KF_PROLOGUE_RMSNORM == kf::kGemvProRmsNorm &&
+                  KF_PROLOGUE_SWIGLU == kf::kGemvProSwiGLU,
+              "prologue codes of the C ABI and the kernels differ");
+static_assert(KF_GEMV_FUSED_MAX_K == kf::kGemvFusedMaxK, "header and kernels disagree on the fused K limit");
 
 namespace {
 
@@ -151,6 +155,30 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
   const kf::GemvPlan plan = kf::gemv_plan(M, ns, ks, count, cus);
   return hip_status(kf::gemv_launch(plan, probs, count, M, group_size, static_cast<hipStream_t>(stream)),
                     "int4_gemv_grouped launch");
+}
+
+int kf_int4_gemv_fused(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
+                       int group_size, int prologue, const void* aux, float eps, const void* residual, void* stream) {
+  int st = check_common(x, packed, scales, y, M, N, K, group_size);
+  if (st) return st;
+  if (M != 1) return fail(KF_ERR_UNSUPPORTED, "int4_gemv_fused handles M = 1 (decode), got M=%d", M);
+  if (prologue < KF_PROLOGUE_NONE || prologue > KF_PROLOGUE_SWIGLU)
+    return fail(KF_ERR_INVALID_ARG, "prologue must be KF_PROLOGUE_NONE, _RMSNORM or _SWIGLU, got %d", prologue);
+  if (prologue != KF_PROLOGUE_NONE && (!aux || !aligned(aux, 16)))
+    return fail(KF_ERR_INVALID_ARG, "the prologue's aux input must be non-null and 16-byte aligned");
+  if (prologue == KF_PROLOGUE_RMSNORM && !(eps >= 0.0f && eps <= 3.0e38f))
+    return fail(KF_ERR_INVALID_ARG, "eps must be finite and >= 0, got %g", (double)eps);
+  if (residual && !aligned(residual, 2)) return fail(KF_ERR_INVALID_ARG, "residual must be 2-byte aligned");
+  if (K > KF_GEMV_FUSED_MAX_K)
+    return fail(KF_ERR_UNSUPPORTED, "int4_gemv_fused needs K <= %d (x in LDS), got K=%d", KF_GEMV_FUSED_MAX_K, K);
+  int cus = 0;
+  if ((st = cu_count(&cus))) return st;
+  const kf::GemvProblem prob = {x, packed, scales, y, N, K};
+  const kf::GemvPlan plan = kf::gemv_plan(1, &N, &K, 1, cus);
+  if (!plan.x_lds) return fail(KF_ERR_UNSUPPORTED, "int4_gemv_fused: x of K=%d does not fit LDS", K);
+  const kf::GemvFused fused = {prologue, aux, eps, residual};
+  return hip_status(kf::gemv_fused_launch(plan, prob, fused, group_size, static_cast<hipStream_t>(stream)),
+                    "int4_gemv_fused launch");
 }
 
 size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size) {

@@ -118,9 +118,9 @@ extern __shared__ __attribute__((aligned(1024))) u32x4 gemv_x_lds[];
 // moves 1 KiB blocks w, w + 4, ... straight from global memory to LDS, no registers involved.
 // Lanes past the end re-read the last piece into the tail of the last block (inside the
 // allocation, which the launcher rounds up to whole 1 KiB blocks).  Completion is awaited
-// with vmcnt in gemv_pass.
-__device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane) {
-  const uint32_t base = (uint32_t)(uintptr_t)gemv_x_lds;
+// with vmcnt in gemv_pass.  `off`: byte offset of the destination in the LDS allocation.
+__device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane, uint32_t off = 0) {
+  const uint32_t base = (uint32_t)(uintptr_t)gemv_x_lds + off;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blocks = (n16 + 63) >> 6;
   for (int b = wave; b < blocks; b += kGemvWavesPerBlock) {
@@ -131,6 +131,83 @@ __device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane) 
   }
 }
 
+// Bytes of LDS one row of x takes (whole 1 KiB blocks, as the copy writes them).
+__device__ __forceinline__ uint32_t x_row_lds_bytes(int K) { return (uint32_t)((2 * K + 1023) & ~1023); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Fused prologues (one row of x, K halves), run by the whole workgroup on its LDS copy once the
+// copies have landed; they end with a barrier.  LDS layout in 16-byte units, xb = one row's
+// blocks: [0, xb) x; RMSNorm: [xb, 2 xb) the norm weight, then 4 partial sums; SwiGLU:
+// [xb, 2 xb) gate, [2 xb, 3 xb) up, and x is written by the prologue.
+//   RMSNorm: x = fp16((x * rsqrt(sum(x^2) / K + eps)) * w), the sum in fp32 in a fixed order
+//            (per thread, then across the wavefront, then wavefronts 0..3).
+//   SwiGLU:  x = fp16(float(fp16(silu(gate))) * up), silu(g) = g / (1 + exp(-g)) in fp32: the
+//            two roundings of torch's silu(gate) * up on fp16 tensors.
+template <int PRO>
+__device__ __forceinline__ void x_prologue(int K, float eps) {
+  const int tid = threadIdx.x;
+  const int k8 = K >> 3;
+  const int xb = (int)(x_row_lds_bytes(K) >> 4);
+  if constexpr (PRO == kGemvProRmsNorm) {
+    const u32x4* w = gemv_x_lds + xb;
+    float* part = reinterpret_cast<float*>(gemv_x_lds + 2 * xb);
+    float ss = 0.0f;
+    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
+      const u32x4 v = gemv_x_lds[p];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half2_t h = bit_cast<half2_t>(v[j]);
+        ss = fmaf((float)h[0], (float)h[0], ss);
+        ss = fmaf((float)h[1], (float)h[1], ss);
+      }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    static_assert(kGemvWavesPerBlock == 4, "four partial sums");
+    const float total = ((part[0] + part[1]) + part[2]) + part[3];
+    const float rstd = rsqrtf(total / (float)K + eps);
+    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
+      const u32x4 v = gemv_x_lds[p], g = w[p];
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half2_t h = bit_cast<half2_t>(v[j]), gw = bit_cast<half2_t>(g[j]);
+        const half2_t r = {(half_t)(((float)h[0] * rstd) * (float)gw[0]), (half_t)(((float)h[1] * rstd) * (float)gw[1])};
+        o[j] = bit_cast<uint32_t>(r);
+      }
+      gemv_x_lds[p] = o;
+    }
+  } else {
+    static_assert(PRO == kGemvProSwiGLU, "prologue kind");
+    const u32x4* gate = gemv_x_lds + xb;
+    const u32x4* up = gemv_x_lds + 2 * xb;
+    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
+      const u32x4 gv = gate[p], uv = up[p];
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half2_t g = bit_cast<half2_t>(gv[j]), u = bit_cast<half2_t>(uv[j]);
+        half2_t r;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float gf = (float)g[e];
+          const half_t sh = (half_t)(gf / (1.0f + expf(-gf)));
+          r[e] = (half_t)((float)sh * (float)u[e]);
+        }
+        o[j] = bit_cast<uint32_t>(r);
+      }
+      gemv_x_lds[p] = o;
+    }
+  }
+  __syncthreads();
+}
+
 template <int R>
 struct RowSet {
   const char* prow[R];  // packed row bases
@@ -139,6 +216,7 @@ struct RowSet {
   int K;
   int chunks;
   int scale_shift;
+  float eps;  // RMSNorm prologue only
 };
 
 // One pass over UU consecutive 64-chunk blocks starting at chunk base cb (uniform).  With
@@ -146,7 +224,7 @@ struct RowSet {
 // vector-memory loads issued after the copy are this pass's UU * R weight and UU * R scale
 // loads, so vmcnt(2 * UU * R) means the copy has landed, and the barrier makes every
 // wavefront's share visible to all.
-template <int M, int R, int UU, bool XLDS>
+template <int M, int R, int UU, bool XLDS, int PRO = kGemvProNone>
 __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane, float (&acc)[M][R], bool first) {
   constexpr int XM = XPrefetch<M>::value;
   u32x4 wv[UU][R];
@@ -175,6 +253,7 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
     if (first) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * UU * R) : "memory");
       __syncthreads();
+      if constexpr (PRO != kGemvProNone) x_prologue<PRO>(rs.K, rs.eps);
     }
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
@@ -232,11 +311,23 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
 // Rows row0 .. row0 + R - 1 of one problem (the body both entry kernels share, so a problem
 // gives the same bits whichever kernel runs it).  Rows past N are clamped to N - 1 for
 // loading and never stored.
-template <int M, int R, int UMAX, bool XLDS>
+template <int M, int R, int UMAX, bool XLDS, int PRO = kGemvProNone>
 __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packed, const half_t* scales,
-                                          half_t* y, int N, int K, int scale_shift, int row0, int lane) {
+                                          half_t* y, int N, int K, int scale_shift, int row0, int lane,
+                                          const half_t* res = nullptr, const half_t* aux = nullptr,
+                                          float eps = 0.0f) {
+  static_assert(PRO == kGemvProNone || (XLDS && M == 1), "fused prologues work on one row of x in LDS");
   if constexpr (XLDS) {
-    stage_x_lds(x, (M * K) >> 3, lane);  // before any other vector-memory load
+    // The copies come before any other vector-memory load.
+    if constexpr (PRO == kGemvProNone) {
+      stage_x_lds(x, (M * K) >> 3, lane);
+    } else if constexpr (PRO == kGemvProRmsNorm) {
+      stage_x_lds(x, K >> 3, lane);
+      stage_x_lds(aux, K >> 3, lane, x_row_lds_bytes(K));
+    } else {
+      stage_x_lds(x, K >> 3, lane, x_row_lds_bytes(K));
+      stage_x_lds(aux, K >> 3, lane, 2 * x_row_lds_bytes(K));
+    }
     // The first pass counts its own weight and scale loads as the only ones issued after the
     // copy.  Loads through __restrict__ arguments could legally be moved past the copy's
     // wait (into the lanes-in-range branch, after the barrier); passing the bases through
@@ -252,6 +343,7 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   rs.K = K;
   rs.chunks = K >> 5;
   rs.scale_shift = scale_shift;
+  rs.eps = eps;
   const size_t row_bytes = (size_t)K >> 1;
   const size_t srow_bytes = (size_t)(rs.chunks >> scale_shift) * 2;
 #pragma unroll
@@ -271,16 +363,16 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
     const int left = rs.chunks - cb;  // uniform
     const bool first = cb == 0;
     if (UMAX >= 4 && left > 192) {
-      gemv_pass<M, R, (UMAX >= 4 ? 4 : 1), XLDS>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 4 ? 4 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
       cb += 256;
     } else if (UMAX >= 3 && left > 128) {
-      gemv_pass<M, R, (UMAX >= 3 ? 3 : 1), XLDS>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 3 ? 3 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
       cb += 192;
     } else if (UMAX >= 2 && left > 64) {
-      gemv_pass<M, R, (UMAX >= 2 ? 2 : 1), XLDS>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 2 ? 2 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
       cb += 128;
     } else {
-      gemv_pass<M, R, 1, XLDS>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, 1, XLDS, PRO>(rs, cb, lane, acc, first);
       cb += 64;
     }
   }
@@ -305,13 +397,22 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   }
   if ((lane & 31) == 31 && (R >= 2 || lane == 31)) {
     const int n = row0 + (lane >> 5);
+    // With a residual: fp16(residual + fp16(result)), the two roundings of adding fp16 tensors.
     if (n < N) {
 #pragma unroll
-      for (int m = 0; m < M; ++m) y[(size_t)m * N + n] = (half_t)(acc[m][0] * kTwoPow24);
+      for (int m = 0; m < M; ++m) {
+        half_t o = (half_t)(acc[m][0] * kTwoPow24);
+        if (res) o = (half_t)((float)res[(size_t)m * N + n] + (float)o);
+        y[(size_t)m * N + n] = o;
+      }
     }
     if (R == 3 && lane == 31 && row0 + 2 < N) {
 #pragma unroll
-      for (int m = 0; m < M; ++m) y[(size_t)m * N + row0 + 2] = (half_t)(acc[m][R - 1] * kTwoPow24);
+      for (int m = 0; m < M; ++m) {
+        half_t o = (half_t)(acc[m][R - 1] * kTwoPow24);
+        if (res) o = (half_t)((float)res[(size_t)m * N + row0 + 2] + (float)o);
+        y[(size_t)m * N + row0 + 2] = o;
+      }
     }
   }
 }
@@ -329,6 +430,17 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const hal
   const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
   if (!XLDS && row0 >= N) return;  // past the last row
   gemv_rows<M, R, UMAX, XLDS>(x, packed, scales, y, N, K, scale_shift, row0, lane);
+}
+
+// One problem at M = 1 with a prologue on x (GemvPrologue) and/or a residual: gemv_kernel with
+// x in LDS, whose copy the prologue transforms before the first product.  y may alias res.
+template <int R, int UMAX, int PRO>
+__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_fused_kernel(
+    const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
+    int N, int K, int scale_shift, const half_t* res, const half_t* __restrict__ aux, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  gemv_rows<1, R, UMAX, true, PRO>(x, packed, scales, y, N, K, scale_shift, row0, lane, res, aux, eps);
 }
 
 // Several problems.  b1 .. b8: first global wavefront of problems 1 .. 8 (ascending; the
@@ -441,6 +553,36 @@ void* pick(int M, const GemvPlan& plan) {
 // Dynamic LDS of the x copy: whole 1 KiB blocks of M * K fp16 values.
 size_t x_lds_bytes(int M, int K) { return (size_t)ceil_div(M * K * 2, 1024) * 1024; }
 
+typedef void (*GemvFusedFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int, const half_t*,
+                            const half_t*, float);
+
+template <int R, int PRO>
+GemvFusedFn pick_fused_u(int U) {
+  switch (U) {
+    case 1: return gemv_fused_kernel<R, 1, PRO>;
+    case 2: return gemv_fused_kernel<R, 2, PRO>;
+    case 3: return gemv_fused_kernel<R, 3, PRO>;
+    default: return gemv_fused_kernel<R, 4, PRO>;
+  }
+}
+
+template <int PRO>
+GemvFusedFn pick_fused_r(int R, int U) { return R == 1 ? pick_fused_u<1, PRO>(U) : pick_fused_u<2, PRO>(U); }
+
+GemvFusedFn pick_fused(int prologue, int R, int U) {
+  switch (prologue) {
+    case kGemvProRmsNorm: return pick_fused_r<kGemvProRmsNorm>(R, U);
+    case kGemvProSwiGLU: return pick_fused_r<kGemvProSwiGLU>(R, U);
+    default: return pick_fused_r<kGemvProNone>(R, U);
+  }
+}
+
+// Dynamic LDS of the fused kernel: x, plus the prologue's inputs (and 4 partial sums).
+size_t fused_lds_bytes(int K, int prologue) {
+  const size_t xb = x_lds_bytes(1, K);
+  return prologue == kGemvProRmsNorm ? 2 * xb + 1024 : (prologue == kGemvProSwiGLU ? 3 * xb : xb);
+}
+
 }  // namespace
 
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
@@ -541,6 +683,19 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
   hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(pick<true>(M, plan)), dim3(blocks),
                      dim3(64 * kGemvWavesPerBlock), lds, stream, count, shift, bounds[0], bounds[1], bounds[2],
                      bounds[3], bounds[4], bounds[5], bounds[6], bounds[7], table);
+  return hipGetLastError();
+}
+
+hipError_t gemv_fused_launch(const GemvPlan& plan, const GemvProblem& q, const GemvFused& f, int group_size,
+                             hipStream_t stream) {
+  const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
+  const int rows = plan.rows_per_wave == 1 ? 1 : 2;  // one problem: never the mixed launch
+  const int blocks = ceil_div(ceil_div(q.N, rows), kGemvWavesPerBlock);
+  hipLaunchKernelGGL(pick_fused(f.prologue, rows, plan.unroll), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
+                     fused_lds_bytes(q.K, f.prologue), stream, static_cast<const half_t*>(q.x),
+                     static_cast<const uint32_t*>(q.packed), static_cast<const half_t*>(q.scales),
+                     static_cast<half_t*>(q.y), q.N, q.K, shift, static_cast<const half_t*>(f.residual),
+                     static_cast<const half_t*>(f.aux), f.eps);
   return hipGetLastError();
 }
 

@@ -62,6 +62,24 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,
                        hipStream_t stream);
 
+// ---- fused decode GEMV (M = 1): a transform of x before the product, a residual after it ----
+// The product is the GEMV's (same kernel body, same bits); the transform runs on the
+// workgroup's LDS copy of x, the residual is added to the fp16 result before its store.
+enum GemvPrologue {
+  kGemvProNone = 0,     // x as given
+  kGemvProRmsNorm = 1,  // x * rsqrt(mean(x^2) + eps) * weight (aux: fp16 weight [K])
+  kGemvProSwiGLU = 2,   // fp16(fp16(silu(gate)) * up) (x: gate [K], aux: up [K])
+};
+constexpr int kGemvFusedMaxK = kGemvMaxLdsX / 2;  // x of the one row fits the LDS budget
+struct GemvFused {
+  int prologue;          // GemvPrologue
+  const void* aux;       // prologue input (see GemvPrologue), else nullptr
+  float eps;             // RMSNorm epsilon
+  const void* residual;  // fp16 [N]: y = fp16(residual + fp16(x @ W_hat^T)); nullptr: no residual
+};
+hipError_t gemv_fused_launch(const GemvPlan& p, const GemvProblem& problem, const GemvFused& f, int group_size,
+                             hipStream_t stream);
+
 // ---- skinny MFMA GEMM (M <= 32, K % 128 == 0): one weight stream, K split in-block ----
 // gemm_plan (kf_gemm.hip) picks it for small M by the measured rule stated there.
 constexpr int kSkinnyMaxM = 32;

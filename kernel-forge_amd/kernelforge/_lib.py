@@ -19,6 +19,10 @@ KF_ERR_INVALID_ARG = 1
 KF_ERR_UNSUPPORTED = 2
 KF_ERR_WORKSPACE = 3
 KF_ERR_HIP = 4
+KF_PROLOGUE_NONE = 0
+KF_PROLOGUE_RMSNORM = 1
+KF_PROLOGUE_SWIGLU = 2
+KF_GEMV_FUSED_MAX_K = 10240
 
 GEMV_MAX_GROUP = 8
 
@@ -38,6 +42,7 @@ SIGNATURES = {
     "kf_last_error": (ctypes.c_char_p, []),
     "kf_int4_gemv": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "kf_int4_gemv_grouped": (_I, [ctypes.POINTER(GemvProblem), _I, _I, _I, _VP]),
+    "kf_int4_gemv_fused": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _VP, ctypes.c_float, _VP, _VP]),
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm_plan": (_I, [_I, _I, _I, _I, _IP, _IP, _IP, _IP, _IP]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),

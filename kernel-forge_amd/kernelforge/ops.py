@@ -389,3 +389,62 @@ def int4_linear(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, gro
     if bias is not None:
         y = y + bias
     return y.reshape(*lead, packed.shape[0])
+
+
+def int4_linear_fused(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128, *,
+                      norm_weight: torch.Tensor | None = None, eps: float = 1e-5, up: torch.Tensor | None = None,
+                      residual: torch.Tensor | None = None) -> torch.Tensor:
+    """A decoder linear with the work around it: ``residual + int4_linear(prologue(x))``.
+
+    prologue: with ``norm_weight``, RMSNorm ``x * rsqrt(mean(x^2) + eps) * norm_weight`` (fp32
+    inside); with ``up``, SwiGLU ``silu(x) * up`` where x is the gate (the fp16 roundings of torch's
+    ``silu(x) * up``); neither: x itself.  ``residual`` ([..., N] fp16), when given, is added to the
+    fp16 result exactly as ``residual + y`` would be.
+
+    At decode size (one row of x, K <= 10240) all of it is one GEMV launch
+    (``kf_int4_gemv_fused``): the prologue runs on the workgroup's LDS copy of x and the residual
+    joins the store, with the product bit-identical to ``int4_linear``'s.  Other sizes run the
+    same steps as separate torch ops around ``int4_linear``.  No reference counterpart.
+    """
+    if norm_weight is not None and up is not None:
+        raise ValueError("int4_linear_fused takes norm_weight or up, not both")
+    lead = x.shape[:-1]
+    k = x.shape[-1]
+    n = packed.shape[0]
+    x2 = x.reshape(-1, k)
+    m = x2.shape[0]
+    res2 = residual.reshape(-1, n) if residual is not None else None
+    if res2 is not None and (res2.shape[0] != m or res2.dtype != torch.float16 or res2.device != x.device):
+        raise ValueError(f"residual must be fp16 [..., {n}] on {x.device} with the leading dims of x")
+    aux = norm_weight if norm_weight is not None else up
+    if aux is not None and (aux.dtype != torch.float16 or aux.device != x.device):
+        raise ValueError("norm_weight / up must be fp16 on the device of x")
+    if up is not None and up.shape != x.shape:
+        raise ValueError(f"up must have the shape of x, {tuple(x.shape)}, got {tuple(up.shape)}")
+    if norm_weight is not None and norm_weight.shape != (k,):
+        raise ValueError(f"norm_weight must be [{k}], got {tuple(norm_weight.shape)}")
+    fused = (m == 1 and k <= _lib.KF_GEMV_FUSED_MAX_K and x.is_cuda and x2.is_contiguous()
+             and x2.data_ptr() % 16 == 0 and (aux is None or (aux.is_contiguous() and aux.data_ptr() % 16 == 0))
+             and (res2 is None or res2.is_contiguous()))
+    if not fused:
+        if norm_weight is not None:
+            x2 = torch.nn.functional.rms_norm(x2, (k,), norm_weight, eps)
+        elif up is not None:
+            x2 = torch.nn.functional.silu(x2) * up.reshape(-1, k)
+        y = int4_linear(x2, packed, scales, group_size)
+        if res2 is not None:
+            y = res2 + y
+        return y.reshape(*lead, n)
+    _check_int4(x2, packed, scales, group_size)
+    _check_native(x2, packed, scales, group_size)
+    prologue = (_lib.KF_PROLOGUE_RMSNORM if norm_weight is not None
+                else _lib.KF_PROLOGUE_SWIGLU if up is not None else _lib.KF_PROLOGUE_NONE)
+    lib = _lib.load()
+    y = torch.empty(1, n, dtype=torch.float16, device=x.device)
+    with torch.cuda.device(x.device):
+        status = lib.kf_int4_gemv_fused(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), 1, n, k, int(group_size),
+                                        prologue, _ptr(aux) if aux is not None else None, float(eps),
+                                        _ptr(res2) if res2 is not None else None, _stream_ptr(x.device))
+    _lib.check(status, "int4_gemv_fused")
+    return y.reshape(*lead, n)
+

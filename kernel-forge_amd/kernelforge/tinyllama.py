@@ -74,6 +74,11 @@ def _rope(x: torch.Tensor, cos: torch.Tensor, sin_signed: torch.Tensor) -> torch
     return torch.addcmul(x * cos, torch.cat([x[..., h:], x[..., :h]], dim=-1), sin_signed)
 
 
+def _int4_fused(lin, x, **kw):
+    """ops.int4_linear_fused on an INT4 layer (KFLinearInt4 or FusedInt4Linear)."""
+    return ops.int4_linear_fused(x, lin.packed, lin.scales, lin.group_size, **kw)
+
+
 class FusedInt4Linear(nn.Module):
     """Several INT4 linears on the same input as ONE GEMV/GEMM over their concatenated rows.
 
@@ -113,20 +118,34 @@ class Attention(nn.Module):
         self.o_proj = nn.Linear(cfg.heads * d, h, bias=False)
         self.qkv: FusedInt4Linear | None = None
 
-    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
-        """x [1, T, H]; pos int64 [T] positions; cos / sin [T, 1, d] RoPE rows of those positions
-        (sin with the rotate-half sign folded in); cache_k / cache_v [kv_heads, max_seq, d] slabs,
-        the key slab holding K transposed ([kv_heads, d, max_seq]); mask [rep * T, max_seq], the
-        additive causal mask repeated for the rep = heads / kv_heads query heads of a KV head."""
+    def project(self, x, norm: "RMSNorm | None" = None):
+        """(q|k [1, T, (heads + kv_heads) d], v [1, T, kv_heads d]) of x.  With `norm` the layers
+        are INT4 and the RMSNorm of x runs inside their GEMV launches (int4_linear_fused)."""
         cfg = self.cfg
-        t = x.shape[1]
-        hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
-        rep = hq // hkv
+        nqk = (cfg.heads + cfg.kv_heads) * cfg.head_dim
+        if norm is not None:
+            kw = dict(norm_weight=norm.weight, eps=norm.eps)
+            if self.qkv is not None:
+                y = _int4_fused(self.qkv, x, **kw)
+                return y[..., :nqk], y[..., nqk:]
+            return (torch.cat([_int4_fused(self.q_proj, x, **kw), _int4_fused(self.k_proj, x, **kw)], dim=-1),
+                    _int4_fused(self.v_proj, x, **kw))
         if self.qkv is not None:
             y = self.qkv.forward_concat(x)                               # [1, T, (hq + 2 hkv) d]
-            qk, v = y[..., :(hq + hkv) * d], y[..., (hq + hkv) * d:]
-        else:
-            qk, v = torch.cat([self.q_proj(x), self.k_proj(x)], dim=-1), self.v_proj(x)
+            return y[..., :nqk], y[..., nqk:]
+        return torch.cat([self.q_proj(x), self.k_proj(x)], dim=-1), self.v_proj(x)
+
+    def core(self, qk, v, pos, cos, sin, cache_k, cache_v, mask):
+        """Attention of the new positions over the cache: [1, T, heads d], before o_proj.
+
+        pos int64 [T] positions; cos / sin [T, 1, d] RoPE rows of those positions (sin with the
+        rotate-half sign folded in); cache_k / cache_v [kv_heads, max_seq, d] slabs, the key slab
+        holding K transposed ([kv_heads, d, max_seq]); mask [rep * T, max_seq], the additive causal
+        mask repeated for the rep = heads / kv_heads query heads of a KV head."""
+        cfg = self.cfg
+        t = qk.shape[1]
+        hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        rep = hq // hkv
         qk = _rope(qk.view(t, hq + hkv, d), cos, sin)                     # q and k heads together
         q, k = qk[:, :hq], qk[:, hq:]
         cache_k.view(hkv, d, cfg.max_seq).index_copy_(2, pos, k.permute(1, 2, 0))
@@ -137,8 +156,12 @@ class Attention(nn.Module):
         scores = torch.baddbmm(mask, qg, cache_k.view(hkv, d, cfg.max_seq), alpha=1.0 / math.sqrt(d))
         probs = torch.softmax(scores, dim=-1)                            # fp32 inside
         out = torch.bmm(probs, cache_v)                                  # [hkv, rep * T, d]
-        out = out.view(hkv, rep, t, d).permute(2, 0, 1, 3).reshape(1, t, hq * d)
-        return self.o_proj(out)
+        return out.view(hkv, rep, t, d).permute(2, 0, 1, 3).reshape(1, t, hq * d)
+
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
+        """x [1, T, H] (already normalized); see core for the other arguments."""
+        qk, v = self.project(x)
+        return self.o_proj(self.core(qk, v, pos, cos, sin, cache_k, cache_v, mask))
 
 
 class MLP(nn.Module):
@@ -149,11 +172,21 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.intermediate, cfg.hidden, bias=False)
         self.gate_up: FusedInt4Linear | None = None
 
-    def forward(self, x):
+    def project(self, x, norm: "RMSNorm | None" = None):
+        """(gate, up) of x; with `norm`, INT4 layers with the RMSNorm inside their GEMV launches."""
+        if norm is not None:
+            kw = dict(norm_weight=norm.weight, eps=norm.eps)
+            if self.gate_up is not None:
+                g, u = torch.split(_int4_fused(self.gate_up, x, **kw), self.gate_up.splits, dim=-1)
+                return g, u
+            return _int4_fused(self.gate_proj, x, **kw), _int4_fused(self.up_proj, x, **kw)
         if self.gate_up is not None:
             g, u = self.gate_up(x)
-        else:
-            g, u = self.gate_proj(x), self.up_proj(x)
+            return g, u
+        return self.gate_proj(x), self.up_proj(x)
+
+    def forward(self, x):
+        g, u = self.project(x)
         return self.down_proj(torch.nn.functional.silu(g) * u)
 
 
@@ -165,9 +198,25 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden, cfg.rms_eps)
         self.mlp = MLP(cfg)
 
+    def int4_fusable(self) -> bool:
+        """Every linear on the INT4 path without bias: the layer can run the fused launches."""
+        a, m = self.self_attn, self.mlp
+        qkv = [a.qkv] if a.qkv is not None else [a.q_proj, a.k_proj, a.v_proj]
+        gu = [m.gate_up] if m.gate_up is not None else [m.gate_proj, m.up_proj]
+        return all(isinstance(p, (KFLinearInt4, FusedInt4Linear)) and getattr(p, "bias", None) is None
+                   for p in qkv + gu + [a.o_proj, m.down_proj])
+
     def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
-        x = x + self.self_attn(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, mask)
-        return x + self.mlp(self.post_attention_layernorm(x))
+        a, m = self.self_attn, self.mlp
+        if self.int4_fusable():
+            # Four INT4 launches per layer at decode: RMSNorm inside q|k|v and gate|up, the residual
+            # adds inside o_proj and down, SiLU-multiply inside down (int4_linear_fused).
+            qk, v = a.project(x, self.input_layernorm)
+            x = _int4_fused(a.o_proj, a.core(qk, v, pos, cos, sin, cache_k, cache_v, mask), residual=x)
+            g, u = m.project(x, self.post_attention_layernorm)
+            return _int4_fused(m.down_proj, g, up=u, residual=x)
+        x = x + a(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, mask)
+        return x + m(self.post_attention_layernorm(x))
 
 
 class TinyLlama(nn.Module):

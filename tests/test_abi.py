@@ -90,3 +90,29 @@ def test_gemm_argument_errors_without_gpu():
     _err(lib.kf_int4_dequant_fp16(None, p, p, 4, 256, 128, None), "non-null")
     _err(lib.kf_bw_copy(p, p, 17, 0, None), "multiple of 16")
     assert lib.kf_int4_gemm_workspace_bytes(0, 64, 256, 128) == 0
+
+
+def test_fused_gemv_argument_errors_without_gpu():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    eps = ctypes.c_float(1e-5)
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 2, 64, 256, 128, 0, None, eps, None, None), "M = 1")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 256, 128, 3, None, eps, None, None), "prologue must be")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 256, 128, _lib.KF_PROLOGUE_RMSNORM, None, eps, None, None),
+         "aux input must be non-null")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 256, 128, _lib.KF_PROLOGUE_SWIGLU, ctypes.c_void_p(0x1008), eps,
+                                None, None), "16-byte aligned")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 256, 128, _lib.KF_PROLOGUE_RMSNORM, p, ctypes.c_float(-1.0),
+                                None, None), "eps must be finite")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 256, 128, 0, None, eps, ctypes.c_void_p(0x1001), None),
+         "residual must be 2-byte aligned")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 10240 + 128, 128, 0, None, eps, None, None), "K <= 10240")
+    _err(lib.kf_int4_gemv_fused(p, p, p, p, 1, 64, 200, 128, 0, None, eps, None, None), "not a multiple of group_size")
+
+
+def test_fused_constants_match_header():
+    text = HEADER.read_text()
+    for name in ("KF_PROLOGUE_NONE", "KF_PROLOGUE_RMSNORM", "KF_PROLOGUE_SWIGLU", "KF_GEMV_FUSED_MAX_K"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert m and int(m.group(1)) == getattr(_lib, name), name
+
