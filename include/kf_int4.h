@@ -101,6 +101,32 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
 int kf_int4_gemv_fused(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
                        int group_size, int prologue, const void* aux, float eps, const void* residual, void* stream);
 
+/* Attention inputs the q|k|v decode GEMV writes directly (kf_int4_gemv_qkv_rope). */
+typedef struct kf_rope_cache {
+  const void* cos;  /* fp16 [max_seq, head_dim] */
+  const void* sin;  /* fp16 [max_seq, head_dim], rotate-half sign folded in: -sin on the first half */
+  const void* pos;  /* int64 in device memory: the token's position (read by the kernel) */
+  void* cache_k;    /* fp16 [kv_heads, head_dim, max_seq]: K transposed */
+  void* cache_v;    /* fp16 [kv_heads, max_seq, head_dim] */
+  int heads;
+  int kv_heads;
+  int head_dim;     /* even */
+  int max_seq;
+} kf_rope_cache;
+
+/* The q|k|v projection of one decode token (M = 1, K <= KF_GEMV_FUSED_MAX_K) with RoPE and the
+ * KV-cache writes in its epilogue, optionally the input RMSNorm in its prologue (norm_weight
+ * non-NULL, as KF_PROLOGUE_RMSNORM).  Rows of packed / scales: heads q heads, kv_heads k heads,
+ * kv_heads v heads, head_dim rows each (N = (heads + 2 kv_heads) * head_dim), i.e. the weights of
+ * q|k|v concatenated.  y [N] receives q and k rotated, v as is, in that order; k is also stored
+ * at cache_k[h][:][pos], v at cache_v[h][pos][:] (skipped when pos is outside [0, max_seq)).
+ * Rotation: fp16(fp16(x * cos) + x_partner * sin), the roundings of x * cos + swap_halves(x) * sin
+ * on fp16 tensors.  No reference counterpart: it fuses the RoPE and cache update that follow the
+ * q|k|v int4_linear calls in a decoder's attention. */
+int kf_int4_gemv_qkv_rope(const void* x, const void* packed, const void* scales, void* y, int N, int K,
+                          int group_size, const void* norm_weight, float eps, const kf_rope_cache* rope,
+                          void* stream);
+
 /* Bytes of fp32 split-K workspace kf_int4_gemm needs for this problem on the
  * current device (0 when the chosen plan has no split-K).
  * Replaces kf::gemm_tc::workspace_floats (dequant_gemm_tc_kernel.cuh:179-183),

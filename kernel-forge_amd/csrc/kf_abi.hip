@@ -181,6 +181,39 @@ int kf_int4_gemv_fused(const void* x, const void* packed, const void* scales, vo
                     "int4_gemv_fused launch");
 }
 
+int kf_int4_gemv_qkv_rope(const void* x, const void* packed, const void* scales, void* y, int N, int K,
+                          int group_size, const void* norm_weight, float eps, const kf_rope_cache* rope,
+                          void* stream) {
+  int st = check_common(x, packed, scales, y, 1, N, K, group_size);
+  if (st) return st;
+  if (!rope) return fail(KF_ERR_INVALID_ARG, "rope must be non-null");
+  const kf_rope_cache& r = *rope;
+  if (!r.cos || !r.sin || !r.pos || !r.cache_k || !r.cache_v)
+    return fail(KF_ERR_INVALID_ARG, "rope: cos, sin, pos, cache_k and cache_v must be non-null");
+  if (!aligned(r.cos, 2) || !aligned(r.sin, 2) || !aligned(r.cache_k, 2) || !aligned(r.cache_v, 2) ||
+      !aligned(r.pos, 8))
+    return fail(KF_ERR_INVALID_ARG, "rope: fp16 tables and caches must be 2-byte, pos 8-byte aligned");
+  if (r.heads < 1 || r.kv_heads < 1 || r.head_dim < 2 || r.head_dim % 2 || r.max_seq < 1)
+    return fail(KF_ERR_INVALID_ARG, "rope: need heads, kv_heads, max_seq >= 1 and an even head_dim, got %d, %d, %d, %d",
+                r.heads, r.kv_heads, r.max_seq, r.head_dim);
+  if ((long long)(r.heads + 2LL * r.kv_heads) * r.head_dim != N)
+    return fail(KF_ERR_INVALID_ARG, "N=%d is not (heads + 2 kv_heads) * head_dim = %lld", N,
+                (long long)(r.heads + 2LL * r.kv_heads) * r.head_dim);
+  if (norm_weight && !aligned(norm_weight, 16)) return fail(KF_ERR_INVALID_ARG, "norm_weight must be 16-byte aligned");
+  if (norm_weight && !(eps >= 0.0f && eps <= 3.0e38f))
+    return fail(KF_ERR_INVALID_ARG, "eps must be finite and >= 0, got %g", (double)eps);
+  if (K > KF_GEMV_FUSED_MAX_K)
+    return fail(KF_ERR_UNSUPPORTED, "int4_gemv_qkv_rope needs K <= %d (x in LDS), got K=%d", KF_GEMV_FUSED_MAX_K, K);
+  int cus = 0;
+  if ((st = cu_count(&cus))) return st;
+  const kf::GemvPlan plan = kf::gemv_plan(1, &N, &K, 1, cus);
+  const kf::GemvProblem prob = {x, packed, scales, y, N, K};
+  const kf::GemvFused fused = {norm_weight ? KF_PROLOGUE_RMSNORM : KF_PROLOGUE_NONE, norm_weight, eps, nullptr};
+  const kf::GemvRope gr = {r.cos, r.sin, r.pos, r.cache_k, r.cache_v, r.heads, r.kv_heads, r.head_dim, r.max_seq};
+  return hip_status(kf::gemv_qkv_rope_launch(prob, fused, gr, plan.unroll, group_size, static_cast<hipStream_t>(stream)),
+                    "int4_gemv_qkv_rope launch");
+}
+
 size_t kf_int4_gemm_workspace_bytes(int M, int N, int K, int group_size) {
   if (M < 1 || N < 1 || K < 64 || K % 64 || (group_size != 64 && group_size != 128)) return 0;
   int cus = 0;

@@ -208,6 +208,42 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
   __syncthreads();
 }
 
+// RoPE + KV-cache epilogue (GemvRope).  tot: after the two-row reduction, lane 31 holds row
+// row0's sum and lane 63 row row0 + step's (2^-24 domain).  For a q or k head, rows row0 and
+// row0 + step are dims j and j + d/2; each is rounded to fp16 and rotated with the roundings of
+// torch's x * cos + swap_halves(x) * sin on fp16 tensors: fp16(fp16(x * cos) + partner * sin).
+// v rows are stored as they are.  The cache writes are skipped for a position outside the cache.
+__device__ __forceinline__ void rope_epilogue(float tot, int lane, int row0, int step, int N, half_t* y,
+                                              const GemvRope& rc) {
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 31));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 63));
+  if ((lane & 31) != 31) return;
+  const int hi = lane >> 5;  // 0: row row0, 1: row row0 + step
+  const int n = row0 + hi * step;
+  if (n >= N) return;
+  const int d = rc.head_dim;
+  const int nrope = (rc.heads + rc.kv_heads) * d;
+  const int64_t p = *static_cast<const int64_t*>(rc.pos);
+  const bool in_cache = p >= 0 && p < rc.max_seq;
+  const size_t prow = (size_t)(in_cache ? p : 0) * d;
+  if (row0 < nrope) {
+    const int head = row0 / d;
+    const int dim = row0 - head * d + hi * (d >> 1);
+    const half_t self = (half_t)((hi ? b : a) * kTwoPow24), other = (half_t)((hi ? a : b) * kTwoPow24);
+    const half_t c = static_cast<const half_t*>(rc.cos)[prow + dim], s = static_cast<const half_t*>(rc.sin)[prow + dim];
+    const half_t t = (half_t)((float)self * (float)c);
+    const half_t o = (half_t)((float)t + (float)other * (float)s);
+    y[n] = o;
+    if (head >= rc.heads && in_cache)
+      static_cast<half_t*>(rc.cache_k)[((size_t)(head - rc.heads) * d + dim) * rc.max_seq + p] = o;
+  } else {
+    const half_t o = (half_t)((hi ? b : a) * kTwoPow24);
+    y[n] = o;
+    const int r = n - nrope, kvh = r / d;
+    if (in_cache) static_cast<half_t*>(rc.cache_v)[((size_t)kvh * rc.max_seq + p) * d + (r - kvh * d)] = o;
+  }
+}
+
 template <int R>
 struct RowSet {
   const char* prow[R];  // packed row bases
@@ -311,11 +347,11 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
 // Rows row0 .. row0 + R - 1 of one problem (the body both entry kernels share, so a problem
 // gives the same bits whichever kernel runs it).  Rows past N are clamped to N - 1 for
 // loading and never stored.
-template <int M, int R, int UMAX, bool XLDS, int PRO = kGemvProNone>
+template <int M, int R, int UMAX, bool XLDS, int PRO = kGemvProNone, bool ROPE = false>
 __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packed, const half_t* scales,
                                           half_t* y, int N, int K, int scale_shift, int row0, int lane,
                                           const half_t* res = nullptr, const half_t* aux = nullptr,
-                                          float eps = 0.0f) {
+                                          float eps = 0.0f, int row_step = 1, const GemvRope* rope = nullptr) {
   static_assert(PRO == kGemvProNone || (XLDS && M == 1), "fused prologues work on one row of x in LDS");
   if constexpr (XLDS) {
     // The copies come before any other vector-memory load.
@@ -348,7 +384,7 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   const size_t srow_bytes = (size_t)(rs.chunks >> scale_shift) * 2;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const size_t n = (size_t)min(row0 + r, N - 1);
+    const size_t n = (size_t)min(row0 + r * row_step, N - 1);
     rs.prow[r] = reinterpret_cast<const char*>(packed) + n * row_bytes;
     rs.srow[r] = reinterpret_cast<const char*>(scales) + n * srow_bytes;
   }
@@ -394,6 +430,11 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
                                                        false);
       acc[m][2] = half_sum_lanes31_63(__uint_as_float(s2[0]) + __uint_as_float(s2[1]));
     }
+  }
+  if constexpr (ROPE) {
+    static_assert(M == 1 && R == 2, "the RoPE epilogue pairs two rows of one x row");
+    rope_epilogue(acc[0][0], lane, row0, row_step, N, y, *rope);
+    return;
   }
   if ((lane & 31) == 31 && (R >= 2 || lane == 31)) {
     const int n = row0 + (lane >> 5);
@@ -441,6 +482,30 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_fused_kernel(
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
   gemv_rows<1, R, UMAX, true, PRO>(x, packed, scales, y, N, K, scale_shift, row0, lane, res, aux, eps);
+}
+
+// The q|k|v decode GEMV with the RoPE + KV-cache epilogue (GemvRope), optionally an RMSNorm
+// prologue.  Wavefront w < (heads + kv_heads) * d / 2 owns dims j, j + d / 2 of head w / (d / 2);
+// the rest own two consecutive v rows.
+template <int UMAX, int PRO>
+__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_qkv_rope_kernel(
+    const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
+    int N, int K, int scale_shift, const half_t* __restrict__ aux, float eps, const GemvRope rope) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half_d = rope.head_dim >> 1;
+  const int nwr = (rope.heads + rope.kv_heads) * half_d;
+  int row0, step;
+  if (w < nwr) {
+    const int head = w / half_d;
+    row0 = head * rope.head_dim + (w - head * half_d);
+    step = half_d;
+  } else {
+    row0 = 2 * nwr + 2 * (w - nwr);
+    step = 1;
+  }
+  gemv_rows<1, 2, UMAX, true, PRO, true>(x, packed, scales, y, N, K, scale_shift, row0, lane, nullptr, aux, eps,
+                                         step, &rope);
 }
 
 // Several problems.  b1 .. b8: first global wavefront of problems 1 .. 8 (ascending; the
@@ -577,6 +642,19 @@ GemvFusedFn pick_fused(int prologue, int R, int U) {
   }
 }
 
+typedef void (*GemvRopeFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int, const half_t*, float,
+                           const GemvRope);
+
+template <int PRO>
+GemvRopeFn pick_rope_u(int U) {
+  switch (U) {
+    case 1: return gemv_qkv_rope_kernel<1, PRO>;
+    case 2: return gemv_qkv_rope_kernel<2, PRO>;
+    case 3: return gemv_qkv_rope_kernel<3, PRO>;
+    default: return gemv_qkv_rope_kernel<4, PRO>;
+  }
+}
+
 // Dynamic LDS of the fused kernel: x, plus the prologue's inputs (and 4 partial sums).
 size_t fused_lds_bytes(int K, int prologue) {
   const size_t xb = x_lds_bytes(1, K);
@@ -683,6 +761,19 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
   hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(pick<true>(M, plan)), dim3(blocks),
                      dim3(64 * kGemvWavesPerBlock), lds, stream, count, shift, bounds[0], bounds[1], bounds[2],
                      bounds[3], bounds[4], bounds[5], bounds[6], bounds[7], table);
+  return hipGetLastError();
+}
+
+hipError_t gemv_qkv_rope_launch(const GemvProblem& q, const GemvFused& f, const GemvRope& rope, int unroll,
+                                int group_size, hipStream_t stream) {
+  const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
+  const int blocks = ceil_div(ceil_div(q.N, 2), kGemvWavesPerBlock);
+  const GemvRopeFn fn = f.prologue == kGemvProRmsNorm ? pick_rope_u<kGemvProRmsNorm>(unroll)
+                                                      : pick_rope_u<kGemvProNone>(unroll);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * kGemvWavesPerBlock), fused_lds_bytes(q.K, f.prologue), stream,
+                     static_cast<const half_t*>(q.x), static_cast<const uint32_t*>(q.packed),
+                     static_cast<const half_t*>(q.scales), static_cast<half_t*>(q.y), q.N, q.K, shift,
+                     static_cast<const half_t*>(f.aux), f.eps, rope);
   return hipGetLastError();
 }
 

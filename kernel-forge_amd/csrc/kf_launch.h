@@ -80,6 +80,21 @@ struct GemvFused {
 hipError_t gemv_fused_launch(const GemvPlan& p, const GemvProblem& problem, const GemvFused& f, int group_size,
                              hipStream_t stream);
 
+// RoPE + KV-cache epilogue of the q|k|v decode GEMV: rows = heads q heads, kv_heads k heads, then
+// kv_heads v heads of head_dim rows each.  A wavefront owns dims j and j + head_dim / 2 of one q or
+// k head, rotates the pair with the position's cos / sin rows, stores it to y (natural order)
+// and, for k, into the key cache; v rows go to y and the value cache.
+struct GemvRope {
+  const void* cos;     // fp16 [max_seq, head_dim]
+  const void* sin;     // fp16 [max_seq, head_dim], rotate-half sign folded in (-sin on the first half)
+  const void* pos;     // int64: the token's position (device memory)
+  void* cache_k;       // fp16 [kv_heads, head_dim, max_seq] (K transposed)
+  void* cache_v;       // fp16 [kv_heads, max_seq, head_dim]
+  int heads, kv_heads, head_dim, max_seq;
+};
+hipError_t gemv_qkv_rope_launch(const GemvProblem& problem, const GemvFused& f, const GemvRope& rope, int unroll,
+                                int group_size, hipStream_t stream);
+
 // ---- skinny MFMA GEMM (M <= 32, K % 128 == 0): one weight stream, K split in-block ----
 // gemm_plan (kf_gemm.hip) picks it for small M by the measured rule stated there.
 constexpr int kSkinnyMaxM = 32;

@@ -37,12 +37,21 @@ class GemvProblem(ctypes.Structure):
 # Every symbol include/kf_int4.h declares, with (restype, argtypes).
 _VP, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _IP = ctypes.POINTER(ctypes.c_int)
+class RopeCache(ctypes.Structure):
+    """kf_rope_cache of include/kf_int4.h."""
+    _fields_ = [("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p), ("pos", ctypes.c_void_p),
+                ("cache_k", ctypes.c_void_p), ("cache_v", ctypes.c_void_p), ("heads", ctypes.c_int),
+                ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("max_seq", ctypes.c_int)]
+
+
 SIGNATURES = {
     "kf_abi_version": (_I, []),
     "kf_last_error": (ctypes.c_char_p, []),
     "kf_int4_gemv": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "kf_int4_gemv_grouped": (_I, [ctypes.POINTER(GemvProblem), _I, _I, _I, _VP]),
     "kf_int4_gemv_fused": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _VP, ctypes.c_float, _VP, _VP]),
+    "kf_int4_gemv_qkv_rope": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _VP, ctypes.c_float, ctypes.POINTER(RopeCache),
+                                   _VP]),
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm_plan": (_I, [_I, _I, _I, _I, _IP, _IP, _IP, _IP, _IP]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),

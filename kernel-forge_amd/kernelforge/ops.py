@@ -448,3 +448,50 @@ def int4_linear_fused(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tenso
     _lib.check(status, "int4_gemv_fused")
     return y.reshape(*lead, n)
 
+
+def int4_qkv_rope_cache(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int, *,
+                        cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor, cache_k: torch.Tensor,
+                        cache_v: torch.Tensor, heads: int, kv_heads: int, head_dim: int,
+                        norm_weight: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """The q|k|v projection of one decode token with RoPE and the KV-cache update in one launch.
+
+    x: one row [..., K] fp16 (RMSNorm-ed first when ``norm_weight`` is given); packed / scales: the
+    q|k|v weights concatenated along N = (heads + 2 kv_heads) head_dim; cos / sin: fp16
+    [max_seq, head_dim] tables (sin with the rotate-half sign folded in: -sin on the first half);
+    pos: int64 [1] on the device; cache_k: fp16 [kv_heads, head_dim, max_seq] (K transposed),
+    cache_v: fp16 [kv_heads, max_seq, head_dim].  Returns y [..., N]: q and k rotated, v as is.
+    k and v are also written at position pos of the caches.  Kernel: kf_int4_gemv_qkv_rope.
+    No reference counterpart.
+    """
+    k = x.shape[-1]
+    n = packed.shape[0]
+    x2 = x.reshape(-1, k)
+    if x2.shape[0] != 1:
+        raise ValueError(f"int4_qkv_rope_cache takes one token, got {x2.shape[0]} rows")
+    if (heads + 2 * kv_heads) * head_dim != n:
+        raise ValueError(f"packed has N={n} rows, not (heads + 2 kv_heads) * head_dim")
+    max_seq = cos.shape[0]
+    for name, t, numel in (("cos", cos, max_seq * head_dim), ("sin", sin, max_seq * head_dim),
+                           ("cache_k", cache_k, kv_heads * head_dim * max_seq),
+                           ("cache_v", cache_v, kv_heads * max_seq * head_dim)):
+        if t.dtype != torch.float16 or not t.is_contiguous() or t.numel() != numel or t.device != x.device:
+            raise ValueError(f"{name} must be a contiguous fp16 tensor of {numel} elements on {x.device}")
+    if pos.dtype != torch.int64 or pos.numel() != 1 or pos.device != x.device:
+        raise ValueError("pos must be one int64 on the device of x")
+    if norm_weight is not None and (norm_weight.dtype != torch.float16 or norm_weight.shape != (k,)
+                                    or not norm_weight.is_contiguous() or norm_weight.data_ptr() % 16):
+        raise ValueError(f"norm_weight must be a contiguous, 16-byte aligned fp16 [{k}]")
+    x2 = x2.contiguous()
+    _check_int4(x2, packed, scales, group_size)
+    _check_native(x2, packed, scales, group_size)
+    lib = _lib.load()
+    y = torch.empty(1, n, dtype=torch.float16, device=x.device)
+    rc = _lib.RopeCache(_ptr(cos), _ptr(sin), _ptr(pos), _ptr(cache_k), _ptr(cache_v), heads, kv_heads, head_dim,
+                        max_seq)
+    with torch.cuda.device(x.device):
+        status = lib.kf_int4_gemv_qkv_rope(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), n, k, int(group_size),
+                                           _ptr(norm_weight) if norm_weight is not None else None, float(eps),
+                                           ctypes.byref(rc), _stream_ptr(x.device))
+    _lib.check(status, "int4_gemv_qkv_rope")
+    return y.reshape(*x.shape[:-1], n)
+

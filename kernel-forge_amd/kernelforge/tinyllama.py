@@ -142,14 +142,25 @@ class Attention(nn.Module):
         rotate-half sign folded in); cache_k / cache_v [kv_heads, max_seq, d] slabs, the key slab
         holding K transposed ([kv_heads, d, max_seq]); mask [rep * T, max_seq], the additive causal
         mask repeated for the rep = heads / kv_heads query heads of a KV head."""
+        return self.attend(self.rope_cache(qk, v, pos, cos, sin, cache_k, cache_v), cache_k, cache_v, mask)
+
+    def rope_cache(self, qk, v, pos, cos, sin, cache_k, cache_v):
+        """RoPE on q and k, k and v written into the caches at `pos`; returns q [T, heads, d]."""
         cfg = self.cfg
         t = qk.shape[1]
         hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
-        rep = hq // hkv
         qk = _rope(qk.view(t, hq + hkv, d), cos, sin)                     # q and k heads together
         q, k = qk[:, :hq], qk[:, hq:]
         cache_k.view(hkv, d, cfg.max_seq).index_copy_(2, pos, k.permute(1, 2, 0))
         cache_v.index_copy_(1, pos, v.view(t, hkv, d).transpose(0, 1))
+        return q
+
+    def attend(self, q, cache_k, cache_v, mask):
+        """q [T, heads, d] (rotated) over the caches: [1, T, heads d], before o_proj."""
+        cfg = self.cfg
+        t = q.shape[0]
+        hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        rep = hq // hkv
         # Query head h reads KV head h // rep: the rep heads of a KV head (and their T positions)
         # form the rows of one batch entry, so K and V are never repeated.
         qg = q.reshape(t, hkv, rep, d).permute(1, 2, 0, 3).reshape(hkv, rep * t, d)
@@ -206,13 +217,25 @@ class DecoderLayer(nn.Module):
         return all(isinstance(p, (KFLinearInt4, FusedInt4Linear)) and getattr(p, "bias", None) is None
                    for p in qkv + gu + [a.o_proj, m.down_proj])
 
-    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask, rope16=None):
+        """rope16: the full fp16 (cos, sin) tables, for the fused q|k|v launch of a decode step."""
         a, m = self.self_attn, self.mlp
         if self.int4_fusable():
             # Four INT4 launches per layer at decode: RMSNorm inside q|k|v and gate|up, the residual
-            # adds inside o_proj and down, SiLU-multiply inside down (int4_linear_fused).
-            qk, v = a.project(x, self.input_layernorm)
-            x = _int4_fused(a.o_proj, a.core(qk, v, pos, cos, sin, cache_k, cache_v, mask), residual=x)
+            # adds inside o_proj and down, SiLU-multiply inside down (int4_linear_fused); with
+            # q|k|v fused, RoPE and the KV-cache writes inside the q|k|v launch as well.
+            ln1 = self.input_layernorm
+            if x.shape[1] == 1 and a.qkv is not None and rope16 is not None:
+                c = a.cfg
+                y = ops.int4_qkv_rope_cache(x, a.qkv.packed, a.qkv.scales, a.qkv.group_size, cos=rope16[0],
+                                            sin=rope16[1], pos=pos, cache_k=cache_k, cache_v=cache_v, heads=c.heads,
+                                            kv_heads=c.kv_heads, head_dim=c.head_dim, norm_weight=ln1.weight,
+                                            eps=ln1.eps)
+                out = a.attend(y[..., :c.heads * c.head_dim].view(1, c.heads, c.head_dim), cache_k, cache_v, mask)
+            else:
+                qk, v = a.project(x, ln1)
+                out = a.core(qk, v, pos, cos, sin, cache_k, cache_v, mask)
+            x = _int4_fused(a.o_proj, out, residual=x)
             g, u = m.project(x, self.post_attention_layernorm)
             return _int4_fused(m.down_proj, g, up=u, residual=x)
         x = x + a(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, mask)
@@ -257,8 +280,9 @@ class TinyLlama(nn.Module):
         # repeated for the query heads that share a KV head.
         c, s = cos[pos].to(x.dtype).unsqueeze(1), sin[pos].to(x.dtype).unsqueeze(1)
         mask_g = mask.to(x.dtype).repeat(self.cfg.heads // self.cfg.kv_heads, 1)
+        rope16 = (cos.to(x.dtype), sin.to(x.dtype)) if x.is_cuda and tokens.numel() == 1 else None
         for i, layer in enumerate(self.layers):
-            x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], mask_g)
+            x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], mask_g, rope16)
         x = self.norm(x[:, -1:])
         return self.lm_head(x).float().view(-1)
 

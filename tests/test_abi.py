@@ -116,3 +116,21 @@ def test_fused_constants_match_header():
         m = re.search(rf"#define {name} (\d+)", text)
         assert m and int(m.group(1)) == getattr(_lib, name), name
 
+
+
+def test_qkv_rope_argument_errors_without_gpu():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    eps = ctypes.c_float(1e-5)
+    rc = _lib.RopeCache(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 32, 4, 64, 160)
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 2048, 128, None, eps, None, None), "rope must be non-null")
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2048, 2048, 128, None, eps, ctypes.byref(rc), None),
+         r"not \(heads \+ 2 kv_heads\) \* head_dim")
+    bad = _lib.RopeCache(0x1000, 0x1000, 0x1004, 0x1000, 0x1000, 32, 4, 64, 160)
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 2048, 128, None, eps, ctypes.byref(bad), None), "8-byte")
+    odd = _lib.RopeCache(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 32, 4, 63, 160)
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2520, 2048, 128, None, eps, ctypes.byref(odd), None), "even head_dim")
+    nul = _lib.RopeCache(0x1000, 0, 0x1000, 0x1000, 0x1000, 32, 4, 64, 160)
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 2048, 128, None, eps, ctypes.byref(nul), None), "non-null")
+    _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 10240 + 128, 128, None, eps, ctypes.byref(rc), None),
+         "K <= 10240")

@@ -172,3 +172,94 @@ def test_argument_errors():
         ops.int4_linear_fused(x, dp, ds, G, norm_weight=x[0, :100])
     with pytest.raises(ValueError, match="residual must be"):
         ops.int4_linear_fused(x, dp, ds, G, residual=x.float())
+
+
+def _rope_tables(s: int, d: int):
+    inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    f = torch.outer(torch.arange(s, dtype=torch.float32), inv)
+    return torch.cat([f, f], -1).cos().half().to(DEV), torch.cat([-f.sin(), f.sin()], -1).half().to(DEV)
+
+
+@pytest.mark.parametrize("heads,kv_heads,d,k,with_norm", [(32, 4, 64, 2048, True), (12, 2, 128, 1536, False),
+                                                           (32, 4, 64, 2048, False)])
+def test_qkv_rope_cache(heads, kv_heads, d, k, with_norm):
+    """q|k|v GEMV with RoPE and the cache writes in its epilogue, against the unfused steps: the
+    GEMV (bit-identical v), torch's x * cos + swap_halves(x) * sin on its fp16 output, index writes."""
+    s_max = 48
+    n = (heads + 2 * kv_heads) * d
+    _, _, dp, ds = _weight(n, k)
+    x = _h(_rng(61).standard_normal((1, 1, k)))
+    w = _h(_rng(62).uniform(0.5, 1.5, k)) if with_norm else None
+    cos, sin = _rope_tables(s_max, d)
+    for p in (0, 17, s_max - 1):
+        pos = torch.tensor([p], dtype=torch.int64, device=DEV)
+        ck = _h(_rng(63 + p).standard_normal((kv_heads, d, s_max)))
+        cv = _h(_rng(64 + p).standard_normal((kv_heads, s_max, d)))
+        ck0, cv0 = ck.clone(), cv.clone()
+        y = ops.int4_qkv_rope_cache(x, dp, ds, G, cos=cos, sin=sin, pos=pos, cache_k=ck, cache_v=cv, heads=heads,
+                                    kv_heads=kv_heads, head_dim=d, norm_weight=w)
+        base = ops.int4_linear_fused(x, dp, ds, G, norm_weight=w).view(n)
+        nqk = (heads + kv_heads) * d
+        assert torch.equal(y.view(n)[nqk:], base[nqk:])                       # v: the GEMV's bits
+        qk = base[:nqk].view(heads + kv_heads, d)
+        rot = torch.addcmul(qk * cos[p], torch.cat([qk[:, d // 2:], qk[:, :d // 2]], -1), sin[p])
+        got = y.view(n)[:nqk].view(heads + kv_heads, d)
+        diff = (got.float() - rot.float()).abs().max().item()
+        assert diff <= 2e-3 * rot.float().abs().max().item(), diff
+        # caches: position p holds exactly what y holds, everything else is untouched
+        kk = got[heads:]                                                       # [kv_heads, d]
+        assert torch.equal(ck[:, :, p], kk)
+        assert torch.equal(cv[:, p, :], y.view(n)[nqk:].view(kv_heads, d))
+        ck[:, :, p] = ck0[:, :, p]
+        cv[:, p, :] = cv0[:, p, :]
+        assert torch.equal(ck, ck0) and torch.equal(cv, cv0)
+
+
+def test_qkv_rope_position_outside_cache_writes_no_cache():
+    heads, kv_heads, d, k, s_max = 8, 2, 64, 1024, 16
+    n = (heads + 2 * kv_heads) * d
+    _, _, dp, ds = _weight(n, k)
+    x = _h(_rng(71).standard_normal((1, k)))
+    cos, sin = _rope_tables(s_max, d)
+    ck = _h(_rng(72).standard_normal((kv_heads, d, s_max)))
+    cv = _h(_rng(73).standard_normal((kv_heads, s_max, d)))
+    ck0, cv0 = ck.clone(), cv.clone()
+    for p in (s_max, -1):
+        pos = torch.tensor([p], dtype=torch.int64, device=DEV)
+        y = ops.int4_qkv_rope_cache(x, dp, ds, G, cos=cos, sin=sin, pos=pos, cache_k=ck, cache_v=cv, heads=heads,
+                                    kv_heads=kv_heads, head_dim=d)
+        assert torch.isfinite(y.float()).all()
+        assert torch.equal(ck, ck0) and torch.equal(cv, cv0)
+
+
+def test_qkv_rope_graph_replays_equal_eager():
+    heads, kv_heads, d, k, s_max = 32, 4, 64, 2048, 40
+    n = (heads + 2 * kv_heads) * d
+    _, _, dp, ds = _weight(n, k)
+    x, w = _h(_rng(81).standard_normal((1, k))), _h(_rng(82).uniform(0.5, 1.5, k))
+    cos, sin = _rope_tables(s_max, d)
+    pos = torch.tensor([5], dtype=torch.int64, device=DEV)
+    ck = torch.zeros(kv_heads, d, s_max, dtype=torch.float16, device=DEV)
+    cv = torch.zeros(kv_heads, s_max, d, dtype=torch.float16, device=DEV)
+
+    def call():
+        return ops.int4_qkv_rope_cache(x, dp, ds, G, cos=cos, sin=sin, pos=pos, cache_k=ck, cache_v=cv, heads=heads,
+                                       kv_heads=kv_heads, head_dim=d, norm_weight=w)
+
+    eager = call()
+    ck_e, cv_e = ck.clone(), cv.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call()
+    for step in range(3):
+        ck.zero_()
+        cv.zero_()
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager) and torch.equal(ck, ck_e) and torch.equal(cv, cv_e), step
