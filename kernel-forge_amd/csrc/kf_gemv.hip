@@ -134,31 +134,35 @@ __device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane, 
 // Bytes of LDS one row of x takes (whole 1 KiB blocks, as the copy writes them).
 __device__ __forceinline__ uint32_t x_row_lds_bytes(int K) { return (uint32_t)((2 * K + 1023) & ~1023); }
 
+// Sum over the 64 lanes, returned to every lane: lanes i and i + 32 paired by permlane32_swap,
+// then the DPP half-wave sum, read from lane 31.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float t = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 31));
 }
 
-// Fused prologues (one row of x, K halves), run by the whole workgroup on its LDS copy once the
-// copies have landed; they end with a barrier.  LDS layout in 16-byte units, xb = one row's
-// blocks: [0, xb) x; RMSNorm: [xb, 2 xb) the norm weight, then 4 partial sums; SwiGLU:
-// [xb, 2 xb) gate, [2 xb, 3 xb) up, and x is written by the prologue.
-//   RMSNorm: x = fp16((x * rsqrt(sum(x^2) / K + eps)) * w), the sum in fp32 in a fixed order
-//            (per thread, then across the wavefront, then wavefronts 0..3).
-//   SwiGLU:  x = fp16(float(fp16(silu(gate))) * up), silu(g) = g / (1 + exp(-g)) in fp32: the
-//            two roundings of torch's silu(gate) * up on fp16 tensors.
+// Fused prologues (one row of x, K halves), run by the whole workgroup on its LDS copies once
+// they have landed; they end with a barrier.  LDS layout in 16-byte units, xb = one row's blocks:
+// [0, xb) x, written here; [xb, 2 xb) the row copied in (x for RMSNorm, gate for SwiGLU);
+// [2 xb, 3 xb) the second input (RMSNorm weight, up).  Writing x to its own region lets every
+// wavefront read the whole input row while others already write, so one barrier suffices.
+//   RMSNorm: x = fp16((x * rsqrt(sum(x^2) / K + eps)) * w); every wavefront sums the whole row in
+//            fp32 in the same order (per lane, then across the wavefront), so all agree.
+//   SwiGLU:  x = fp16(float(fp16(silu(gate))) * up), silu(g) = g * rcp(1 + exp(-g)) with the
+//            hardware exp and reciprocal (about 1 ulp of fp32 each, far below the fp16 rounding
+//            that follows), and torch's two fp16 roundings of silu(gate) * up.
 template <int PRO>
 __device__ __forceinline__ void x_prologue(int K, float eps) {
   const int tid = threadIdx.x;
   const int k8 = K >> 3;
   const int xb = (int)(x_row_lds_bytes(K) >> 4);
+  const u32x4* in = gemv_x_lds + xb;
+  const u32x4* in2 = gemv_x_lds + 2 * xb;
   if constexpr (PRO == kGemvProRmsNorm) {
-    const u32x4* w = gemv_x_lds + xb;
-    float* part = reinterpret_cast<float*>(gemv_x_lds + 2 * xb);
     float ss = 0.0f;
-    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
-      const u32x4 v = gemv_x_lds[p];
+    for (int p = tid & 63; p < k8; p += 64) {
+      const u32x4 v = in[p];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const half2_t h = bit_cast<half2_t>(v[j]);
@@ -166,14 +170,9 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
         ss = fmaf((float)h[1], (float)h[1], ss);
       }
     }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) part[tid >> 6] = ss;
-    __syncthreads();
-    static_assert(kGemvWavesPerBlock == 4, "four partial sums");
-    const float total = ((part[0] + part[1]) + part[2]) + part[3];
-    const float rstd = rsqrtf(total / (float)K + eps);
+    const float rstd = rsqrtf(wave_sum(ss) / (float)K + eps);
     for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
-      const u32x4 v = gemv_x_lds[p], g = w[p];
+      const u32x4 v = in[p], g = in2[p];
       u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -185,10 +184,8 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
     }
   } else {
     static_assert(PRO == kGemvProSwiGLU, "prologue kind");
-    const u32x4* gate = gemv_x_lds + xb;
-    const u32x4* up = gemv_x_lds + 2 * xb;
     for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
-      const u32x4 gv = gate[p], uv = up[p];
+      const u32x4 gv = in[p], uv = in2[p];
       u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -197,7 +194,7 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const float gf = (float)g[e];
-          const half_t sh = (half_t)(gf / (1.0f + expf(-gf)));
+          const half_t sh = (half_t)(gf * __builtin_amdgcn_rcpf(1.0f + __expf(-gf)));
           r[e] = (half_t)((float)sh * (float)u[e]);
         }
         o[j] = bit_cast<uint32_t>(r);
@@ -357,10 +354,7 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
     // The copies come before any other vector-memory load.
     if constexpr (PRO == kGemvProNone) {
       stage_x_lds(x, (M * K) >> 3, lane);
-    } else if constexpr (PRO == kGemvProRmsNorm) {
-      stage_x_lds(x, K >> 3, lane);
-      stage_x_lds(aux, K >> 3, lane, x_row_lds_bytes(K));
-    } else {
+    } else {  // the row and the second input go past the x region, which the prologue writes
       stage_x_lds(x, K >> 3, lane, x_row_lds_bytes(K));
       stage_x_lds(aux, K >> 3, lane, 2 * x_row_lds_bytes(K));
     }
@@ -655,10 +649,10 @@ GemvRopeFn pick_rope_u(int U) {
   }
 }
 
-// Dynamic LDS of the fused kernel: x, plus the prologue's inputs (and 4 partial sums).
+// Dynamic LDS of the fused kernel: x, plus the prologue's two inputs.
 size_t fused_lds_bytes(int K, int prologue) {
   const size_t xb = x_lds_bytes(1, K);
-  return prologue == kGemvProRmsNorm ? 2 * xb + 1024 : (prologue == kGemvProSwiGLU ? 3 * xb : xb);
+  return prologue == kGemvProNone ? xb : 3 * xb;
 }
 
 }  // namespace
