@@ -94,7 +94,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-m2048", action="store_true", help="skip the M=2048 GEMM leg")
-    ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "copy"],
+    ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "copy", "decode"],
                     help="only launch one kernel --profile-iters times (for rocprofv3 --pmc runs) and exit")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
@@ -151,6 +151,8 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
     gemm_m2048:  the MFMA GEMM on the gate shape at M=2048.
     copy:        kf_bw_copy of 64 MiB (64 MiB read + 64 MiB written per launch), the known-size
       kernel that calibrates FETCH_SIZE / WRITE_SIZE.
+    decode:      the INT4 TinyLlama of the e2e leg: 16-token prompt, capture, --profile-iters graph
+      replays of the decode step (for a kernel trace of one token).
     """
     stream = torch.cuda.current_stream().cuda_stream
     if args.profile == "copy":
@@ -159,6 +161,14 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
         b = torch.empty_like(a)
         for _ in range(args.profile_iters):
             kl.check(lib.kf_bw_copy(a.data_ptr(), b.data_ptr(), nbytes, 0, stream), "copy")
+    elif args.profile == "decode":
+        from kernelforge import tinyllama as tl
+        cfg = tl.TinyLlamaConfig()
+        dec = tl.GraphDecoder(tl.build_int4_model(cfg, "cuda", seed=0), "cuda")
+        gen = torch.Generator(device="cuda").manual_seed(1)
+        dec.prefill(torch.randint(0, cfg.vocab, (16,), device="cuda", generator=gen))
+        dec.capture()
+        dec.decode(args.profile_iters)
     elif args.profile == "gemm_m2048":
         layers = make_layers(torch, kq)
         gate = [ly for ly in layers if ly["name"] == "gate"][0]
