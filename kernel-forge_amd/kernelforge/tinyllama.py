@@ -278,9 +278,13 @@ class TinyLlama(nn.Module):
         x = self.embed_tokens(tokens).unsqueeze(0)
         # Per-token inputs shared by every layer: RoPE rows of the positions, and the mask
         # repeated for the query heads that share a KV head.
-        c, s = cos[pos].to(x.dtype).unsqueeze(1), sin[pos].to(x.dtype).unsqueeze(1)
         mask_g = mask.to(x.dtype).repeat(self.cfg.heads // self.cfg.kv_heads, 1)
         rope16 = (cos.to(x.dtype), sin.to(x.dtype)) if x.is_cuda and tokens.numel() == 1 else None
+        # The per-position rows are only needed by layers that apply RoPE in torch.
+        if rope16 is not None and all(ly.int4_fusable() and ly.self_attn.qkv is not None for ly in self.layers):
+            c = s = None
+        else:
+            c, s = cos[pos].to(x.dtype).unsqueeze(1), sin[pos].to(x.dtype).unsqueeze(1)
         for i, layer in enumerate(self.layers):
             x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], mask_g, rope16)
         x = self.norm(x[:, -1:])
@@ -319,7 +323,8 @@ class GraphDecoder:
     def __init__(self, model: TinyLlama, device):
         self.model, self.device = model, device
         cfg = model.cfg
-        self.rope = _rope_tables(cfg, device)
+        # fp16 tables: the per-token casts in the model's forward are then no-ops.
+        self.rope = tuple(t.to(model.embed_tokens.weight.dtype) for t in _rope_tables(cfg, device))
         self.cache = model.new_cache(device)
         self.token = torch.zeros(1, dtype=torch.long, device=device)
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
