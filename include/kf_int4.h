@@ -119,7 +119,8 @@ typedef struct kf_rope_cache {
  * non-NULL, as KF_PROLOGUE_RMSNORM).  Rows of packed / scales: heads q heads, kv_heads k heads,
  * kv_heads v heads, head_dim rows each (N = (heads + 2 kv_heads) * head_dim), i.e. the weights of
  * q|k|v concatenated.  y [N] receives q and k rotated, v as is, in that order; k is also stored
- * at cache_k[h][:][pos], v at cache_v[h][pos][:] (skipped when pos is outside [0, max_seq)).
+ * at cache_k[h][:][pos], v at cache_v[h][pos][:].  A pos outside [0, max_seq) writes no cache entry
+ * and rotates q and k in y with row 0 of the tables (no table row exists for it).
  * Rotation: fp16(fp16(x * cos) + x_partner * sin), the roundings of x * cos + swap_halves(x) * sin
  * on fp16 tensors.  No reference counterpart: it fuses the RoPE and cache update that follow the
  * q|k|v int4_linear calls in a decoder's attention. */

@@ -209,7 +209,8 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
 // row0's sum and lane 63 row row0 + step's (2^-24 domain).  For a q or k head, rows row0 and
 // row0 + step are dims j and j + d/2; each is rounded to fp16 and rotated with the roundings of
 // torch's x * cos + swap_halves(x) * sin on fp16 tensors: fp16(fp16(x * cos) + partner * sin).
-// v rows are stored as they are.  The cache writes are skipped for a position outside the cache.
+// v rows are stored as they are.  A position outside the cache writes no cache entry and rotates
+// with the tables' row 0 (the read stays in bounds).
 __device__ __forceinline__ void rope_epilogue(float tot, int lane, int row0, int step, int N, half_t* y,
                                               const GemvRope& rc) {
   const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 31));

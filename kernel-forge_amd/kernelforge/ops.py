@@ -460,7 +460,8 @@ def int4_qkv_rope_cache(x: torch.Tensor, packed: torch.Tensor, scales: torch.Ten
     [max_seq, head_dim] tables (sin with the rotate-half sign folded in: -sin on the first half);
     pos: int64 [1] on the device; cache_k: fp16 [kv_heads, head_dim, max_seq] (K transposed),
     cache_v: fp16 [kv_heads, max_seq, head_dim].  Returns y [..., N]: q and k rotated, v as is.
-    k and v are also written at position pos of the caches.  Kernel: kf_int4_gemv_qkv_rope.
+    k and v are also written at position pos of the caches; a pos outside [0, max_seq) writes no
+    cache entry (and rotates with the tables' row 0).  Kernel: kf_int4_gemv_qkv_rope.
     No reference counterpart.
     """
     k = x.shape[-1]
