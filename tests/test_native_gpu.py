@@ -30,8 +30,11 @@ def test_native_check(variant):
     print(r.stdout[-4000:], r.stderr[-4000:])
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "OK (0 failures)" in r.stdout
-    # Both groups: the GEMM at M in {1, 3, 8, 9, 16, 17, 33, 64, 65}, the GEMV at the three M <= 8.
-    assert r.stdout.count("err=") == 2 * (9 + 3)
+    # Both groups: the GEMM at M in {1, 3, 8, 9, 16, 17, 33, 64, 65}, the GEMV at the three M <= 8,
+    # and the fused decode GEMV's two prologues.
+    assert r.stdout.count(" err=") == 2 * (9 + 3 + 2)
+    assert r.stdout.count("fused residual bit-exact=1") == 2
+    assert r.stdout.count("v bit-exact=1 cache=1") == 2
 
 
 def test_native_check_links():
