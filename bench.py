@@ -23,12 +23,14 @@ Protocol
 * Infinity-Cache-cold: R copies of the 7-layer weight set (R * 22.8 MB >= 2x
   the 256 MB MALL) are rotated, step i using copy i % R.
 * Steps are captured in HIP graphs (R steps per graph; host launch cost is
-  excluded, as in the reference's CUDA-graph decode); W warm-up steps, then
-  exactly K timed steps bracketed by torch.cuda.synchronize().
-* roofline: the dominant kernel is the grouped GEMV (the whole step).  Its
-  average duration per launch is measured live with a HIP event pair around
-  graph replays of back-to-back launches (rotating copies) on the launching
-  stream; achieved = 22,779,904 B / that duration.
+  excluded, as in the reference's CUDA-graph decode).  Every graph is captured
+  before timing; then W warm-up steps and exactly K timed steps, bracketed by
+  torch.cuda.synchronize() and timed by a HIP event pair on the launching
+  stream behind a short GPU spin (the reference's launch guard).  The host wall
+  clock over the same K steps is reported beside it.
+* roofline: the dominant kernel is the grouped GEMV (the whole step, one launch
+  per step), so its average duration per launch is the timed region's event
+  time / K; achieved = 22,779,904 B / that duration.
 * reference_protocol: the same step timed the reference's way
   (kernelforge/bench_utils.py:114-185): 50 eager calls, each behind a GPU spin
   guard and between its own event pair; median / p10 / p90 per call.  It
@@ -44,8 +46,11 @@ Protocol
   TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum, each beside
   hipBLASLt's dense fp16 GEMM on the same shape (torch F.linear with fp16
   weights, same protocol).
-* cpu_baseline: the oracle's FP32 dequant + matmul (numpy; the reference's
-  CPU path restated) on the host cores over a bounded sample.
+* cpu_baseline: the reference's FP32 dequant + matmul restated in torch
+  (oracle/cpu_baseline.py) on the host cores over a bounded sample, per call
+  and matmul-only.
+* --headline-only: only the ceilings and the timed step (the command whose
+  rocprofv3 kernel trace backs roofline.avg_launch_us).
 
 --gpus N > 1 is refused: this build measures one GPU.
 """
@@ -100,6 +105,8 @@ def parse_args():
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--no-e2e", action="store_true", help="skip the TinyLlama graph-decode leg (config 5)")
     ap.add_argument("--no-quant", action="store_true", help="skip the on-device quantize leg")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the ceilings and the timed grouped step (the command profiles/ traces)")
     return ap.parse_args()
 
 
@@ -163,7 +170,9 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
             kl.check(lib.kf_bw_copy(a.data_ptr(), b.data_ptr(), nbytes, 0, stream), "copy")
     elif args.profile == "decode":
         from kernelforge import tinyllama as tl
-        cfg = tl.TinyLlamaConfig()
+        import dataclasses
+
+        cfg = dataclasses.replace(tl.TinyLlamaConfig(), max_seq=16 + args.profile_iters + 3)
         dec = tl.GraphDecoder(tl.build_int4_model(cfg, "cuda", seed=0), "cuda")
         gen = torch.Generator(device="cuda").manual_seed(1)
         dec.prefill(torch.randint(0, cfg.vocab, (16,), device="cuda", generator=gen))
@@ -251,8 +260,28 @@ def _timed_ms(fn) -> float:
     return (time.perf_counter() - t0) * 1e3
 
 
+_SPIN_CYCLES_PER_MS = None
+
+
+def spin_cycles_per_ms(torch) -> float:
+    """Cycles of torch.cuda._sleep per millisecond, from one timed 1M-cycle spin (cached)."""
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        torch.cuda._sleep(100_000)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        torch.cuda._sleep(1_000_000)
+        e.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_MS = 1_000_000 / max(s.elapsed_time(e), 1e-3)
+    return _SPIN_CYCLES_PER_MS
+
+
 class GraphSteps:
-    """Runs `count` steps as replays of captured graphs; step i uses weight copy i % copies."""
+    """Runs `count` steps as replays of captured graphs; step i uses weight copy i % copies.
+
+    Graphs are built by prepare(); run() only replays, so a timed run() never captures or
+    instantiates a graph (it raises if one is missing)."""
 
     def __init__(self, torch, step_fn, copies: int):
         self.torch, self.step_fn, self.copies = torch, step_fn, copies
@@ -265,33 +294,58 @@ class GraphSteps:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
 
-    def _graph(self, n: int):
-        if n not in self.graphs:
-            g = self.torch.cuda.CUDAGraph()
-            with self.torch.cuda.graph(g):
-                for r in range(n):
-                    self.step_fn(r)
-            self.graphs[n] = g
-        return self.graphs[n]
+    def _sizes(self, count: int) -> list[int]:
+        full, rem = divmod(count, self.copies)
+        return [self.copies] * full + ([rem] if rem else [])
+
+    def prepare(self, count: int) -> None:
+        """Captures every graph run(count) replays."""
+        for n in set(self._sizes(count)):
+            if n not in self.graphs:
+                g = self.torch.cuda.CUDAGraph()
+                with self.torch.cuda.graph(g):
+                    for r in range(n):
+                        self.step_fn(r)
+                self.graphs[n] = g
+        self.torch.cuda.synchronize()
 
     def run(self, count: int) -> None:
-        full, rem = divmod(count, self.copies)
-        for _ in range(full):
-            self._graph(self.copies).replay()
-        if rem:
-            self._graph(rem).replay()
+        sizes = self._sizes(count)
+        missing = sorted({n for n in sizes if n not in self.graphs})
+        if missing:
+            raise RuntimeError(f"GraphSteps.run({count}): graphs of {missing} steps not prepared")
+        for n in sizes:
+            self.graphs[n].replay()
 
-    def event_avg_ms(self, count: int) -> float:
-        """Average time per step from one HIP event pair on the launching stream."""
+    def timed(self, count: int, guard_ms: float = 0.2) -> tuple[float, float]:
+        """(ms per step from a HIP event pair on the launching stream, wall-clock ms per step),
+        both over exactly `count` replayed steps bracketed by synchronize().
+
+        A GPU spin of `guard_ms` runs before the start event (the reference's launch guard,
+        kernelforge/bench_utils.py:114-185), so the replays are already queued when the start
+        event fires and host launch latency does not count as GPU time.  The wall clock runs
+        from the first enqueue to the final synchronize, minus the spin."""
         torch = self.torch
-        self.run(count)  # make sure every graph used below exists
+        self.prepare(count)
+        cycles = int(guard_ms * spin_cycles_per_ms(torch))
         torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g, s, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        t0 = time.perf_counter()
+        g.record()
+        torch.cuda._sleep(cycles)
         s.record()
         self.run(count)
         e.record()
         torch.cuda.synchronize()
-        return s.elapsed_time(e) / count
+        wall_ms = (time.perf_counter() - t0) * 1e3 - g.elapsed_time(s)
+        return s.elapsed_time(e) / count, wall_ms / count
+
+    def event_avg_ms(self, count: int) -> float:
+        """Average time per step from one HIP event pair on the launching stream (after one
+        untimed run of the same count)."""
+        self.prepare(count)
+        self.run(count)
+        return self.timed(count)[0]
 
 
 def reference_protocol(torch, fn, copies: int, iters: int = 50, warmup: int = 10,
@@ -311,13 +365,7 @@ def reference_protocol(torch, fn, copies: int, iters: int = 50, warmup: int = 10
         fn(i % copies)
     host_ms = (time.perf_counter() - t0) * 1e3 / 5
     torch.cuda.synchronize()
-    # Spin-kernel cycles per ms, from one timed spin.
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    torch.cuda._sleep(1_000_000)
-    e.record()
-    torch.cuda.synchronize()
-    cycles_per_ms = 1_000_000 / max(s.elapsed_time(e), 1e-3)
+    cycles_per_ms = spin_cycles_per_ms(torch)
     guard_ms = max(1.0, 5.0 * host_ms + 0.5)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
@@ -426,6 +474,82 @@ def make_layers(torch, kq, shapes=TL_LAYERS, seed=1000):
     return layers
 
 
+def environment(torch, props) -> dict:
+    """Software and clock/power state of the box the line was measured on."""
+    env = {"device": props.name, "gcn_arch": getattr(props, "gcnArchName", None),
+           "cu_count": props.multi_processor_count, "hbm_gib": round(props.total_memory / 2**30, 1),
+           "torch": torch.__version__, "torch_hip": torch.version.hip}
+    try:
+        env["rocm"] = Path("/opt/rocm/.info/version").read_text().strip()
+    except OSError:
+        env["rocm"] = None
+    for key, cmd in (("amd_smi_metric", ["amd-smi", "metric", "-g", "0", "-p", "-c", "--json"]),
+                     ("amd_smi_driver", ["amd-smi", "static", "-g", "0", "--driver", "--json"])):
+        try:
+            out = subprocess.run(cmd, capture_output=True, text=True, timeout=30)
+            env[key] = json.loads(out.stdout) if out.returncode == 0 else f"exit {out.returncode}"
+        except (OSError, subprocess.SubprocessError, ValueError) as exc:
+            env[key] = f"unavailable: {type(exc).__name__}"
+    return env
+
+
+def host_enqueue_us(torch, fn, calls: int = 200) -> float:
+    """Host time per eager call (launch enqueue, no synchronization), median of 5 batches."""
+    for _ in range(20):
+        fn()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        per.append((time.perf_counter() - t0) * 1e6 / calls)
+        torch.cuda.synchronize()
+    return round(statistics.median(per), 2)
+
+
+def cpu_baseline(torch, layers, step_bytes: int, seconds: float) -> dict:
+    """The reference's CPU FP32 dequant + matmul (oracle/cpu_baseline.py, torch on the host cores)
+    over a bounded sample of the workload: the 7 TinyLlama linears at M=1.  Threads: every core
+    in this process's affinity set, capped by OMP_NUM_THREADS where the box sets it (its CPU
+    share); both counts are recorded."""
+    from oracle import cpu_baseline as cb
+
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(affinity, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else affinity
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        host = [(ly["x"], ly["packed"], ly["scales"]) for ly in layers]
+        w_hats = [cb.dequantize_fp32(p, s, GROUP) for _, p, s in host]
+
+        def sample(fn, budget):
+            for i, (x, p, s) in enumerate(host):  # warm-up
+                fn(i, x, p, s)
+            times, t_end = [], time.perf_counter() + budget
+            while time.perf_counter() < t_end or len(times) < 5:
+                t1 = time.perf_counter()
+                for i, (x, p, s) in enumerate(host):
+                    fn(i, x, p, s)
+                times.append(time.perf_counter() - t1)
+            return statistics.median(times), len(times)
+
+        full, n_full = sample(lambda i, x, p, s: cb.linear_fp32(x, p, s, GROUP), 0.7 * seconds)
+        mm, n_mm = sample(lambda i, x, p, s: cb.matmul_only(x, w_hats[i]), 0.3 * seconds)
+    finally:
+        torch.set_num_threads(saved)
+    return {"value": round(step_bytes / full / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n_full} steps of the 7 TinyLlama linears at M=1, FP32 dequant + matmul per call "
+                      f"(torch on {threads} threads: unpack, q*s, x.float() @ W_hat.T); "
+                      f"median {full * 1e3:.2f} ms/step",
+            "us_per_step": round(full * 1e6, 1),
+            "matmul_only": {"value": round(step_bytes / mm / 1e9, 3), "unit": "GB/s", "us_per_step": round(mm * 1e6, 1),
+                            "steps": n_mm, "note": "x.float() @ W_hat.T on W_hat dequantized once"},
+            "affinity_cores": affinity, "os_cpu_count": os.cpu_count(), "omp_num_threads": omp,
+            "cpu_model": _cpu_model()}
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -433,8 +557,9 @@ def main() -> int:
         print(f"bench.py measures a single GPU: --gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
               "This build has no multi-GPU path; run with --gpus 1.", file=sys.stderr)
         return 2
+    full = not args.headline_only
     traffic = None
-    if not args.profile and not args.no_traffic:
+    if full and not args.profile and not args.no_traffic:
         log("rocprofv3 FETCH_SIZE / WRITE_SIZE passes (child processes)")
         traffic = measure_traffic()
         log(f"traffic: {traffic}")
@@ -493,68 +618,78 @@ def main() -> int:
             single(r, nm)
 
     # --- the timed step (value): one grouped launch over the 7 linears --------------------------
+    # Every graph the warm-up and the timed run replay is captured first; the timed region then
+    # only replays (W warm-up steps, then exactly K steps between synchronize() calls), timed by
+    # a HIP event pair on the launching stream, with the host's wall clock beside it.
     log(f"{copies} weight copies ({copies * set_bytes / 2**20:.0f} MiB); warmup {args.warmup} steps")
     main_steps = GraphSteps(torch, step_grouped, copies)
+    main_steps.prepare(args.warmup)
+    main_steps.prepare(args.steps)
     main_steps.run(args.warmup)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    main_steps.run(args.steps)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
+    ms_per_step, wall_ms_per_step = main_steps.timed(args.steps)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"grouped 7-layer step {ms_per_step * 1e3:.2f} us -> {value:.0f} GB/s")
+    log(f"grouped 7-layer step {ms_per_step * 1e3:.3f} us (events; wall clock {wall_ms_per_step * 1e3:.3f} us) "
+        f"-> {value:.0f} GB/s")
 
     # --- roofline of the dominant kernel (the grouped GEMV: one launch per step) ----------------
-    gemv_avg_ms = main_steps.event_avg_ms(8 * copies)
-    achieved = step_bytes / (gemv_avg_ms * 1e-3) / 1e9
-    log(f"grouped GEMV avg {gemv_avg_ms * 1e3:.2f} us per launch -> {achieved:.0f} GB/s")
-    # The same step timed the reference's way: one eager call per event pair, behind a spin guard.
-    ref_proto = reference_protocol(torch, step_grouped, copies)
-    ref_proto["gbps_at_median"] = round(step_bytes / (ref_proto["median_us"] * 1e-6) / 1e9, 1)
-    log(f"reference protocol (per-call events): median {ref_proto['median_us']} us, "
-        f"p10 {ref_proto['p10_us']}, p90 {ref_proto['p90_us']}")
+    # achieved: the timed region's own event average (one launch per step); a longer event run
+    # of 8 x copies steps is reported beside it.
+    achieved = value
+    long_avg_ms = main_steps.event_avg_ms(8 * copies)
+    log(f"grouped GEMV: {ms_per_step * 1e3:.3f} us per launch in the timed region, {long_avg_ms * 1e3:.3f} us over "
+        f"{8 * copies} launches")
 
-    # --- the other step structures ----------------------------------------------------------------
-    structures = {}
-    for label, fn, launches in (("decoder_4_launches", step_decoder, 4), ("separate_7_launches", step_separate, 7)):
-        gs = GraphSteps(torch, fn, copies)
-        ms = gs.event_avg_ms(8 * copies)
-        structures[label] = {"launches": launches, "us_per_step": round(ms * 1e3, 3),
-                             "gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-                             "pct_of_copy": round(100 * step_bytes / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
-        log(f"{label}: {ms * 1e3:.2f} us/step")
-    per_layer = {}
-    for nm in names:
-        i = idx[nm]
-        gs = GraphSteps(torch, lambda r, nm=nm: single(r, nm), copies)
-        ms = gs.event_avg_ms(8 * copies)
-        b = algo_bytes(1, layers[i]["N"], layers[i]["K"])
-        per_layer[nm] = {"N": layers[i]["N"], "K": layers[i]["K"], "bytes": b, "us": round(ms * 1e3, 3),
-                         "gbps": round(b / (ms * 1e-3) / 1e9, 1),
-                         "pct_of_copy": round(100 * b / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
+    ref_proto = structures = per_layer = qwen = host_us = None
+    if full:
+        # The same step timed the reference's way: one eager call per event pair, behind a spin guard.
+        ref_proto = reference_protocol(torch, step_grouped, copies)
+        ref_proto["gbps_at_median"] = round(step_bytes / (ref_proto["median_us"] * 1e-6) / 1e9, 1)
+        log(f"reference protocol (per-call events): median {ref_proto['median_us']} us, "
+            f"p10 {ref_proto['p10_us']}, p90 {ref_proto['p90_us']}")
+        host_us = {"int4_linear_gate": host_enqueue_us(torch, lambda: single(0, "gate")),
+                   "int4_linear_grouped_7": host_enqueue_us(torch, lambda: step_grouped(0))}
+        log(f"host enqueue per eager call: {host_us}")
 
-    # --- config 3: the Qwen2.5-1.5B decoder linears as one grouped launch ------------------------
-    qlayers = make_layers(torch, kq, QWEN_LAYERS, seed=2000)
-    q_bytes = sum(algo_bytes(1, ly["N"], ly["K"]) for ly in qlayers)
-    q_set = sum(ly["packed"].numel() * 4 + ly["scales"].numel() * 2 for ly in qlayers)
-    q_copies = max(2, -(-(2 * MALL_BYTES) // q_set))
-    q_dev = [[(ly["packed"].cuda(), ly["scales"].cuda()) for ly in qlayers] for _ in range(q_copies)]
-    q_xs = [ly["x"].cuda() for ly in qlayers]
-    gs = GraphSteps(torch, lambda r: ops.int4_linear_grouped(q_xs, [p for p, _ in q_dev[r]], [s for _, s in q_dev[r]],
-                                                             GROUP), q_copies)
-    q_ms = gs.event_avg_ms(8 * q_copies)
-    q_gbps = q_bytes / (q_ms * 1e-3) / 1e9
-    qwen = {"workload": "qwen2.5_1.5b_7_linears_m1_g128", "shapes_NxK": [[n, k] for _, n, k in QWEN_LAYERS],
-            "bytes_per_step": q_bytes, "us_per_step": round(q_ms * 1e3, 3), "gbps": round(q_gbps, 1),
-            "pct_of_measured_copy": round(100 * q_gbps / ceil["hbm_copy_gbps"], 1),
-            "reference_pct_of_copy_on_its_gpu": REFERENCE_QWEN_PCT_OF_COPY, "weight_copies_rotated": q_copies}
-    log(f"Qwen2.5 grouped 7-layer step {q_ms * 1e3:.2f} us -> {q_gbps:.0f} GB/s")
-    del gs, q_dev
+        # --- the other step structures ------------------------------------------------------------
+        structures = {}
+        for label, fn, launches in (("decoder_4_launches", step_decoder, 4), ("separate_7_launches", step_separate, 7)):
+            gs = GraphSteps(torch, fn, copies)
+            ms = gs.event_avg_ms(8 * copies)
+            structures[label] = {"launches": launches, "us_per_step": round(ms * 1e3, 3),
+                                 "gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                                 "pct_of_copy": round(100 * step_bytes / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
+            log(f"{label}: {ms * 1e3:.2f} us/step")
+        per_layer = {}
+        for nm in names:
+            i = idx[nm]
+            gs = GraphSteps(torch, lambda r, nm=nm: single(r, nm), copies)
+            ms = gs.event_avg_ms(8 * copies)
+            b = algo_bytes(1, layers[i]["N"], layers[i]["K"])
+            per_layer[nm] = {"N": layers[i]["N"], "K": layers[i]["K"], "bytes": b, "us": round(ms * 1e3, 3),
+                             "gbps": round(b / (ms * 1e-3) / 1e9, 1),
+                             "pct_of_copy": round(100 * b / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
+
+        # --- config 3: the Qwen2.5-1.5B decoder linears as one grouped launch --------------------
+        qlayers = make_layers(torch, kq, QWEN_LAYERS, seed=2000)
+        q_bytes = sum(algo_bytes(1, ly["N"], ly["K"]) for ly in qlayers)
+        q_set = sum(ly["packed"].numel() * 4 + ly["scales"].numel() * 2 for ly in qlayers)
+        q_copies = max(2, -(-(2 * MALL_BYTES) // q_set))
+        q_dev = [[(ly["packed"].cuda(), ly["scales"].cuda()) for ly in qlayers] for _ in range(q_copies)]
+        q_xs = [ly["x"].cuda() for ly in qlayers]
+        gs = GraphSteps(torch, lambda r: ops.int4_linear_grouped(q_xs, [p for p, _ in q_dev[r]],
+                                                                 [s for _, s in q_dev[r]], GROUP), q_copies)
+        q_ms = gs.event_avg_ms(8 * q_copies)
+        q_gbps = q_bytes / (q_ms * 1e-3) / 1e9
+        qwen = {"workload": "qwen2.5_1.5b_7_linears_m1_g128", "shapes_NxK": [[n, k] for _, n, k in QWEN_LAYERS],
+                "bytes_per_step": q_bytes, "us_per_step": round(q_ms * 1e3, 3), "gbps": round(q_gbps, 1),
+                "pct_of_measured_copy": round(100 * q_gbps / ceil["hbm_copy_gbps"], 1),
+                "reference_pct_of_copy_on_its_gpu": REFERENCE_QWEN_PCT_OF_COPY, "weight_copies_rotated": q_copies}
+        log(f"Qwen2.5 grouped 7-layer step {q_ms * 1e3:.2f} us -> {q_gbps:.0f} GB/s")
+        del gs, q_dev
 
     # --- M=2048: MFMA GEMM on every shape ------------------------------------------------------
     m2048 = None
-    if not args.no_m2048:
+    if full and not args.no_m2048:
         log("M=2048 GEMM leg")
         mfma_peak = measure_mfma_peak(torch)
         # Beside each INT4 layer: hipBLASLt's dense fp16 GEMM on the same shape (torch F.linear,
@@ -569,10 +704,12 @@ def main() -> int:
             bsteps = GraphSteps(torch, lambda r, xm=xm, wd=wd: torch.nn.functional.linear(xm, wd), 10)
             tb = statistics.median(bsteps.event_avg_ms(10) for _ in range(5))
             fl = 2.0 * 2048 * ly["N"] * ly["K"]
+            plan = ops.gemm_plan(2048, ly["N"], ly["K"], GROUP)
             per[ly["name"]] = {"us": round(t * 1e3, 1), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
                                "hipblaslt_fp16_us": round(tb * 1e3, 1),
                                "hipblaslt_fp16_tflops": round(fl / (tb * 1e-3) / 1e12, 1),
-                               "int4_over_hipblaslt_fp16": round(tb / t, 3)}
+                               "int4_over_hipblaslt_fp16": round(tb / t, 3),
+                               "plan": {"kernel": plan["kernel"], "splits": plan["splits"], "tile": plan["tile"]}}
             total_flops += fl
             total_ms += t
             blas_ms += tb
@@ -589,7 +726,7 @@ def main() -> int:
 
     # --- on-device quantize + pack of an fp32 gate weight (format producer) --------------------
     quant = None
-    if not args.no_quant:
+    if full and not args.no_quant:
         log("quantize leg")
         qn, qk = 5632, 2048
         in_bytes, out_bytes = qn * qk * 4, qn * qk // 2 + 2 * qn * (qk // GROUP)
@@ -610,38 +747,18 @@ def main() -> int:
 
     # --- config 5: end-to-end graph decode ------------------------------------------------------
     e2e = None
-    if not args.no_e2e:
+    if full and not args.no_e2e:
         log("TinyLlama graph decode leg")
         e2e = e2e_decode(torch)
         log(f"decode tok/s: int4 fused {e2e['int4_fused_tok_s']}, unfused {e2e['int4_unfused_tok_s']}, "
             f"fp16 {e2e['fp16_tok_s']}")
 
-    # --- CPU baseline: the oracle's FP32 dequant + matmul on the host cores --------------------
+    # --- CPU baseline: the reference's FP32 dequant + matmul on the host cores ------------------
     cpu = None
-    if not args.no_cpu:
-        from threadpoolctl import threadpool_limits
-
-        from oracle import int4_oracle as o
-
-        threads = min(len(os.sched_getaffinity(0)), 16)
-        host = [(ly["packed"].numpy(), ly["scales"].numpy(), ly["x"].numpy()) for ly in layers]
-        with threadpool_limits(limits=threads):
-            for p, s, x in host:  # warm-up
-                o.linear_ref_fp32(x, p, s, GROUP)
-            times = []
-            t_end = time.perf_counter() + args.cpu_seconds
-            while time.perf_counter() < t_end or len(times) < 3:
-                t1 = time.perf_counter()
-                for p, s, x in host:
-                    o.linear_ref_fp32(x, p, s, GROUP)
-                times.append(time.perf_counter() - t1)
-        med = statistics.median(times)
-        cpu = {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{len(times)} steps of the 7 TinyLlama linears at M=1 (oracle FP32 dequant+matmul, "
-                         f"numpy; BLAS on {threads} threads, nibble unpack single-threaded); "
-                         f"median {med * 1e3:.1f} ms/step",
-               "cpu_model": _cpu_model()}
-        log(f"CPU baseline {cpu['value']} GB/s ({med * 1e3:.1f} ms/step)")
+    if full and not args.no_cpu:
+        cpu = cpu_baseline(torch, layers, step_bytes, args.cpu_seconds)
+        log(f"CPU baseline {cpu['value']} GB/s ({cpu['us_per_step']} us/step on {cpu['cores']} threads); "
+            f"matmul only {cpu['matmul_only']['value']} GB/s")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -651,6 +768,9 @@ def main() -> int:
                    "group_size": GROUP, "bytes_per_step": step_bytes, "weight_copies_rotated": copies,
                    "step": "one int4_linear_grouped launch over the 7 independent linears",
                    "graph_captured": True},
+        "timer": {"ms_per_step": "HIP event pair on the launching stream around the K replayed steps, "
+                                 "between synchronize() calls; every graph captured before the timed region",
+                  "wall_ms_per_step": round(wall_ms_per_step, 6)},
         "pct_of_measured_copy": round(100 * value / ceil["hbm_copy_gbps"], 1),
         "pct_of_measured_read": round(100 * value / ceil["hbm_read_gbps"], 1),
         "reference_pct_of_copy_on_its_gpu": REFERENCE_PCT_OF_COPY,
@@ -658,14 +778,16 @@ def main() -> int:
                      "frac": round(achieved / SPEC_HBM_GBPS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,
                      "traffic_detail": traffic,
-                     "kernel": "kf::gemv_grouped_kernel<1,3,1,x in LDS> (7 TinyLlama linears; gate at 3 rows per wavefront)",
-                     "bytes_per_launch": step_bytes, "avg_launch_us": round(gemv_avg_ms * 1e3, 3),
+                     "kernel": "kf::gemv_grouped_kernel (7 TinyLlama linears; gate at 3 rows per wavefront)",
+                     "bytes_per_launch": step_bytes, "avg_launch_us": round(ms_per_step * 1e3, 3),
+                     "avg_launch_us_over_8x_copies": round(long_avg_ms * 1e3, 3),
                      "frac_of_measured_copy": round(achieved / ceil["hbm_copy_gbps"], 4),
                      "frac_of_measured_read": round(achieved / ceil["hbm_read_gbps"], 4),
                      "same_size_read": same_read,
                      "frac_of_same_size_read": round(achieved / same_read["gbps"], 4)},
         "cpu_baseline": cpu,
         "reference_protocol": ref_proto,
+        "host_enqueue_us": host_us,
         "ceilings": {k: round(v, 1) if isinstance(v, float) else v for k, v in ceil.items()},
         "step_structures": structures,
         "per_layer_m1": per_layer,
@@ -673,7 +795,7 @@ def main() -> int:
         "m2048": m2048,
         "e2e_decode": e2e,
         "quantize": quant,
-        "device": props.name, "cu_count": props.multi_processor_count,
+        "environment": environment(torch, props) if full else None,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -317,7 +317,9 @@ class GraphDecoder:
 
     The captured step reads the current token and position from static device tensors, runs
     the model, writes argmax into the token buffer and the output history, and advances the
-    position, so replays need no host round trip.
+    position, so replays need no host round trip.  The host keeps its own count of the position
+    and refuses (ValueError) a prefill, capture or decode whose steps would write past the last
+    history / cache slot (max_seq - 1): a step at position p writes history[p + 1].
     """
 
     def __init__(self, model: TinyLlama, device):
@@ -330,6 +332,14 @@ class GraphDecoder:
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
         self.history = torch.zeros(cfg.max_seq, dtype=torch.long, device=device)
         self.graph = None
+        self.host_pos = 0
+
+    def _reserve(self, steps: int, what: str) -> None:
+        """Raises unless `steps` more steps from the current position stay inside max_seq."""
+        last = self.model.cfg.max_seq - 1
+        if self.host_pos + steps > last:
+            raise ValueError(f"{what}: {steps} step(s) from position {self.host_pos} would write position "
+                             f"{self.host_pos + steps}, past max_seq - 1 = {last}")
 
     def _step(self):
         mask = causal_mask(self.pos, self.model.cfg.max_seq)
@@ -342,6 +352,8 @@ class GraphDecoder:
     def prefill(self, prompt: torch.Tensor) -> None:
         """Runs the prompt eagerly; leaves the first generated token in self.token."""
         t = prompt.numel()
+        if not 0 < t < self.model.cfg.max_seq:
+            raise ValueError(f"prefill: a prompt of {t} tokens needs 0 < t < max_seq = {self.model.cfg.max_seq}")
         pos = torch.arange(t, device=self.device)
         self.cache.zero_()
         logits = self.model(prompt, pos, self.cache, self.rope, causal_mask(pos, self.model.cfg.max_seq))
@@ -350,8 +362,10 @@ class GraphDecoder:
         self.token.copy_(torch.argmax(logits).view(1))
         self.history[t] = self.token[0]
         self.pos.fill_(t)
+        self.host_pos = t
 
     def capture(self) -> None:
+        self._reserve(2, "capture (two warm-up steps)")
         saved = (self.cache.clone(), self.token.clone(), self.pos.clone(), self.history.clone())
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -369,6 +383,8 @@ class GraphDecoder:
         self.history.copy_(saved[3])
 
     def decode(self, steps: int, use_graph: bool = True) -> torch.Tensor:
+        self._reserve(steps, "decode")
+        self.host_pos += steps
         for _ in range(steps):
             if use_graph:
                 self.graph.replay()

@@ -8,6 +8,9 @@ package never imports it.
   int4_oracle.py   numpy restatement (quantize, pack/unpack, dequantize, FP32 reference)
   kf_oracle.c      C restatement of the reference's torch-free LCG workload
   c_oracle.py      ctypes binding of libkf_oracle.so (built by oracle/Makefile)
+  cpu_baseline.py  the reference's CPU FP32 dequant + matmul in torch (bench.py's cpu_baseline leg)
 
-Parity of every function is pinned in tests/test_oracle.py; none is "parity unpinned".
+Every function is pinned in tests/test_oracle.py (KATs, exact rational arithmetic, brute force,
+the C restatement; quantization_error on a crafted weight with exact errors); none is
+"parity unpinned".
 """

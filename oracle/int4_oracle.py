@@ -44,6 +44,10 @@ How each function is pinned (tests/test_oracle.py):
   scales; dequantize_fp32 is exact (checked against float64).
 * linear_ref_fp32 / linear_ref_f64: against each other and against a brute
   force triple loop on tiny shapes, plus linearity in x.
+* quantization_error: on a crafted weight whose per-element errors are exact
+  rationals (tests/exact_cases.py): max_abs_err exactly, rmse and rel_fro_err
+  against the exact values' square roots (a missing sqrt, a sum for a mean or
+  a max without abs fails), bits_per_weight = 4 + 16/G.
 * lcg_workload: against the C restatement bit for bit.
 * reorder_mfma16: against a per-element loop that follows the header's wording
   (lane l of block (b, s): row 16b + l%16, words 16s + 4(l/16) .. +3), and as a

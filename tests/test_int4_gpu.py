@@ -152,6 +152,32 @@ def test_grouped_gemv_bit_identical_to_single(error_log, m, group):
         assert err <= REL_TOL, f"{name}: {err:.3e}"
 
 
+QWEN_SEVEN = [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 1536),
+              ("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960)]
+
+
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_qwen_seven_as_benchmarked(error_log, group):
+    """BASELINE config 3 exactly as bench.py times it: the 7 Qwen2.5-1.5B linears in one grouped
+    launch at M = 1 (mixed two- and three-row wavefronts), each output bit-identical to its own
+    GEMV launch and within tolerance of the oracle."""
+    xs, ps, ss, refs = [], [], [], []
+    for i, (_, n, k) in enumerate(QWEN_SEVEN):
+        packed, scales, dp, ds = _weights(n, k, group)
+        x = _x(1, k, 3000 + i)
+        xs.append(torch.from_numpy(x).to(DEV))
+        ps.append(dp)
+        ss.append(ds)
+        refs.append(o.linear_ref_fp32(x, packed, scales, group))
+    ys = ops.int4_linear_grouped(xs, ps, ss, group)
+    for i, (name, n, k) in enumerate(QWEN_SEVEN):
+        assert torch.equal(ys[i], ops.int4_gemv(xs[i], ps[i], ss[i], group)), f"qwen {name}: grouped != single"
+        err = o.max_rel_err(ys[i].float().cpu().numpy(), refs[i])
+        error_log.add("int4_gemv_grouped", case=f"qwen_seven_{name}", shape=[1, n, k], group=group,
+                      max_rel_err=err, passed=err <= REL_TOL)
+        assert err <= REL_TOL, f"qwen {name}: {err:.3e}"
+
+
 @pytest.mark.parametrize("shapes,m_leads", [
     ([(9, 256), (129, 512), (64, 4160), (1, 128)], [(1, 1), (2, 3)]),  # ragged N at M <= 8: GEMV fallback
     ([(64, 256), (192, 512), (128, 4160)], [(2, 5), (33,)]),            # M > GEMV_MAX_M: per-problem GEMM
@@ -234,6 +260,35 @@ def test_edge_shapes_reach_every_tile_and_split():
 @pytest.mark.parametrize("m", [1, 8, 9, 128])
 def test_matmul_dispatcher(error_log, m):
     _check(error_log, "int4_matmul", ops.int4_matmul, m, 2048, 2048, 128, "dispatch")
+
+
+CONFIG4_M = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 2048]
+
+
+@pytest.mark.parametrize("m", CONFIG4_M)
+@pytest.mark.parametrize("layer", ["tinyllama_gate_up", "tinyllama_down"])
+def test_matmul_config4_grid(error_log, layer, m):
+    """BASELINE config 4 in full: int4_matmul (the dispatcher the op calls) on TinyLlama gate and
+    down at every M of the crossover sweep, whichever kernel it picks, against the oracle."""
+    n, k = LAYER_SHAPES[layer]
+    _check(error_log, "int4_matmul", ops.int4_matmul, m, n, k, 128, f"config4_{layer}")
+
+
+@pytest.mark.parametrize("mfma16", [True, False], ids=["mfma16_copy", "public_layout"])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("layer", ["tinyllama_gate_up", "tinyllama_down"])
+def test_gemm_small_m_both_layouts(error_log, monkeypatch, layer, m, mfma16):
+    """The skinny MFMA kernel int4_matmul runs at 3 <= M <= 7 (and int4_gemm at M = 2), reading the
+    cached MFMA-16 copy or the public layout, against the oracle on config 4's gate and down."""
+    n, k = LAYER_SHAPES[layer]
+    monkeypatch.setattr(ops, "MFMA16_CACHE", mfma16)
+    assert ops.gemm_plan(m, n, k, 128)["kernel"] == "skinny"
+    _, _, dp, _ = _weights(n, k, 128)
+    out = _check(error_log, "int4_gemm", ops.int4_gemm, m, n, k, 128, f"small_m_{layer}_{'mfma16' if mfma16 else 'public'}")
+    assert (getattr(dp, ops._MFMA16_ATTR, None) is not None) or not mfma16
+    if m > ops.GEMV_MAX_M:  # the op's own route at this M is the same kernel
+        x = torch.from_numpy(_x(m, k, m * 7 + n + k)).to(DEV)
+        assert torch.equal(ops.int4_matmul(x, dp, _weights(n, k, 128)[3], 128), out)
 
 
 def test_matmul_ragged_n_follows_the_reference_dispatch():
@@ -431,6 +486,34 @@ def test_custom_op_registered_and_fake():
         fx = mode.from_tensor(x)
         fy = torch.ops.kernelforge.int4_matmul(fx, mode.from_tensor(dp), mode.from_tensor(ds), 128)
         assert tuple(fy.shape) == (4, 64) and fy.dtype == torch.float16
+
+
+@pytest.mark.parametrize("m,n", [(1, 5632), (4, 256), (7, 100), (64, 2048)])
+def test_eager_path_equals_the_registered_op(m, n):
+    """int4_linear / int4_linear_grouped call the ops' implementations directly in eager mode; the
+    results equal the registered kernelforge::int4_matmul(_grouped) ops bit for bit, and errors
+    come out the same (GEMV for ragged N at M <= 7, the GEMM's rejection at M = 8)."""
+    k = 2048
+    _, _, dp, ds = _weights(n, k, 128)
+    x = torch.from_numpy(_x(m, k, 5 + m)).to(DEV)
+    assert torch.equal(ops.int4_linear(x, dp, ds, 128), torch.ops.kernelforge.int4_matmul(x, dp, ds, 128))
+    ys = ops.int4_linear_grouped([x, x], [dp, dp], [ds, ds], 128)
+    yo = torch.ops.kernelforge.int4_matmul_grouped([x, x], [dp, dp], [ds, ds], 128)
+    assert all(torch.equal(a, b) for a, b in zip(ys, yo))
+    if n % 64:
+        with pytest.raises(ValueError, match="multiple of 64"):
+            ops.int4_linear(torch.from_numpy(_x(8, k, 1)).to(DEV), dp, ds, 128)
+
+
+def test_int4_linear_compiles_through_the_registered_op():
+    """Under torch.compile the op (with its fake impl) is what int4_linear calls."""
+    _, _, dp, ds = _weights(256, 2048, 128)
+    x = torch.from_numpy(_x(2, 2048, 77)).to(DEV)
+
+    def f(a):
+        return ops.int4_linear(a, dp, ds, 128) * 2
+
+    assert torch.equal(torch.compile(f, backend="eager", fullgraph=True)(x), f(x))
 
 
 def test_quantize_linears_swaps_decoder_linears():

@@ -19,6 +19,7 @@ import pytest
 
 from oracle import c_oracle
 from oracle import int4_oracle as o
+from exact_cases import crafted_error_case
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
@@ -188,6 +189,26 @@ def test_quantizer_invariants_and_error_stats():
         assert stats["bits_per_weight"] == pytest.approx(4 + 16 / g)
 
 
+def test_quantization_error_exact_on_crafted_weight():
+    """max_abs_err, rmse, rel_fro_err and bits_per_weight against exact rational values."""
+    import math
+
+    w, errs = crafted_error_case()
+    packed, scales = o.quantize_weight(w, 64)
+    stats = o.quantization_error(w, packed, scales, 64)
+    max_abs = max(abs(e) for e in errs)
+    assert max_abs == 1 and min(errs) == -max_abs  # the largest error is negative
+    mean_sq = sum(e * e for e in errs) / len(errs)
+    w_sq = sum(Fraction(float(v)) ** 2 for v in w.ravel())
+    assert stats["max_abs_err"] == float(max_abs)
+    assert stats["rmse"] == pytest.approx(math.sqrt(mean_sq), rel=1e-12)
+    assert stats["rel_fro_err"] == pytest.approx(math.sqrt(sum(e * e for e in errs) / w_sq), rel=1e-6)
+    assert stats["bits_per_weight"] == 8.0 * (packed.size * 4 + scales.size * 2) / w.size == 4 + 16 / 64
+    # rmse is a root of a mean: neither the mean square nor the root of the sum
+    assert abs(stats["rmse"] - float(mean_sq)) > 1e-3
+    assert abs(stats["rmse"] - math.sqrt(sum(e * e for e in errs))) > 1e-3
+
+
 def test_quantizer_rejections():
     with pytest.raises(ValueError, match="not a multiple of group_size"):
         o.quantize_weight(np.zeros((16, 200), dtype=np.float32), 128)
@@ -351,3 +372,27 @@ def test_reorder_mfma16_is_a_permutation():
     assert (counts[:-1] == k // 32).all() and counts[-1] == (32 - n + 1) * (k // 32)  # rows 21..31 repeat row 20
     with pytest.raises(ValueError):
         o.reorder_mfma16(packed[:, :12], scales[:, :1], 128)  # K = 96
+
+
+# ---------------------------------------------------------------------------
+# The torch restatement timed as bench.py's CPU baseline (oracle/cpu_baseline.py)
+# ---------------------------------------------------------------------------
+
+def test_cpu_baseline_matches_numpy_oracle():
+    """Unpack and fp32 dequant bit-exact against the pinned numpy oracle (every nibble value at
+    every position, plus a seeded weight); the matmul within fp32 summation-order tolerance."""
+    import torch
+
+    from oracle import cpu_baseline as cb
+
+    q = np.array([[u - 8 for u in range(16)] * 8], dtype=np.int8).reshape(16, 8)
+    q = np.concatenate([np.roll(q, s, axis=1) for s in range(8)], axis=0)  # every value at every k offset
+    packed = o.pack_int4(q)
+    assert np.array_equal(cb.unpack_int4(torch.from_numpy(packed)).numpy(), q)
+    _, x, packed, scales = o.seeded_case(3, 200, 1024, 128, seed=5)
+    tp, ts = torch.from_numpy(packed), torch.from_numpy(scales)
+    assert np.array_equal(cb.dequantize_fp32(tp, ts, 128).numpy(), o.dequantize_fp32(packed, scales, 128))
+    y = cb.linear_fp32(torch.from_numpy(x), tp, ts, 128).numpy()
+    assert o.max_rel_err(y, o.linear_ref_f64(x, packed, scales, 128)) < 1e-5
+    w_hat = cb.dequantize_fp32(tp, ts, 128)
+    assert np.array_equal(cb.matmul_only(torch.from_numpy(x), w_hat).numpy(), y)

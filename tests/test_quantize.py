@@ -53,6 +53,35 @@ def test_quantization_error_is_bounded(group_size):
     assert stats["bits_per_weight"] == pytest.approx(4 + 16 / group_size)
 
 
+def test_quantization_error_matches_oracle_and_exact_values():
+    """kernelforge.quantize.quantization_error (torch, fp32) against the oracle's (numpy, float64
+    rmse) and the exact rational errors of a crafted weight; then against the oracle on a seeded
+    gaussian weight (reference kernelforge/quantize.py:117-126)."""
+    import math
+
+    from exact_cases import crafted_error_case
+
+    w, errs = crafted_error_case()
+    qw = kq.quantize_weight(torch.from_numpy(w), 64)
+    stats = kq.quantization_error(torch.from_numpy(w), qw)
+    ref = o.quantization_error(w, qw.packed.numpy(), qw.scales.numpy(), 64)
+    assert stats["max_abs_err"] == ref["max_abs_err"] == float(max(abs(e) for e in errs))
+    assert stats["rmse"] == pytest.approx(math.sqrt(sum(e * e for e in errs) / len(errs)), rel=1e-6)
+    assert stats["rmse"] == pytest.approx(ref["rmse"], rel=1e-6)
+    assert stats["rel_fro_err"] == pytest.approx(ref["rel_fro_err"], rel=1e-6)
+    assert stats["bits_per_weight"] == ref["bits_per_weight"] == 4 + 16 / 64
+    g = torch.Generator().manual_seed(3)
+    wg = torch.randn(96, 512, generator=g) * 0.02
+    for gs in (64, 128):
+        qg = kq.quantize_weight(wg, gs)
+        a = kq.quantization_error(wg, qg)
+        b = o.quantization_error(wg.numpy(), qg.packed.numpy(), qg.scales.numpy(), gs)
+        assert a["max_abs_err"] == b["max_abs_err"]
+        for key in ("rmse", "rel_fro_err"):
+            assert a[key] == pytest.approx(b[key], rel=1e-5)
+        assert a["bits_per_weight"] == b["bits_per_weight"]
+
+
 def test_absmax_maps_to_seven_and_zero_groups_are_safe():
     w = torch.zeros(2, 128)
     w[0, 5] = -3.5

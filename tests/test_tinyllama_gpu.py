@@ -40,16 +40,9 @@ def test_fused_qkv_gateup_bit_identical():
     assert torch.equal(a, b)
 
 
-@torch.no_grad()
-def test_logits_match_cpu_fp32_reference():
-    """First-token logits of the INT4 fp16 model vs the same network in fp32 on the CPU with
-    W_hat = q * s from the oracle (only the activation precision differs)."""
-    cfg = _small_cfg()
-    model = tl.build_int4_model(cfg, DEV, seed=2, fuse=False)  # fusion itself: test above
-    prompt = _prompt(12, cfg.vocab)
-    pos = torch.arange(12, device=DEV)
-    got = model(prompt, pos, model.new_cache(DEV), tl._rope_tables(cfg, DEV), tl.causal_mask(pos, cfg.max_seq))
-
+def _cpu_fp32_reference(model, cfg):
+    """The same network in fp32 on the CPU with W_hat = q * s from the oracle for every INT4 linear
+    (only the activation precision differs from the GPU model)."""
     ref_model = tl.TinyLlama(cfg).float()
     sd = {k: v.float().cpu() for k, v in model.state_dict().items() if "packed" not in k and "scales" not in k}
     ref_model.load_state_dict(sd, strict=False)
@@ -61,13 +54,88 @@ def test_logits_match_cpu_fp32_reference():
             ref_mods[name].weight.data = torch.from_numpy(w)
             n_int4 += 1
     assert n_int4 == 7 * cfg.layers
+    return ref_model
+
+
+def _cpu_logits(ref_model, cfg, tokens):
     cpu = torch.device("cpu")
-    ref = ref_model(prompt.cpu(), pos.cpu(), ref_model.new_cache(cpu, torch.float32), tl._rope_tables(cfg, cpu),
-                    tl.causal_mask(pos.cpu(), cfg.max_seq))
-    got = got.cpu()
-    rel = (got - ref).abs().max() / ref.abs().max()
+    pos = torch.arange(tokens.numel())
+    return ref_model(tokens.cpu(), pos, ref_model.new_cache(cpu, torch.float32), tl._rope_tables(cfg, cpu),
+                     tl.causal_mask(pos, cfg.max_seq))
+
+
+def _rel(a, b):
+    return ((a.float().cpu() - b.float().cpu()).abs().max() / b.float().cpu().abs().max()).item()
+
+
+@torch.no_grad()
+def test_logits_match_cpu_fp32_reference():
+    """First-token logits of the INT4 fp16 model (prefill, M = 12 rows through int4_linear) vs the
+    CPU fp32 model on the oracle's W_hat."""
+    cfg = _small_cfg()
+    model = tl.build_int4_model(cfg, DEV, seed=2, fuse=False)  # fusion itself: test above
+    prompt = _prompt(12, cfg.vocab)
+    pos = torch.arange(12, device=DEV)
+    got = model(prompt, pos, model.new_cache(DEV), tl._rope_tables(cfg, DEV), tl.causal_mask(pos, cfg.max_seq))
+    ref = _cpu_logits(_cpu_fp32_reference(model, cfg), cfg, prompt)
+    rel = _rel(got, ref)
     assert rel < 2e-2, f"logits rel err {rel:.3e}"
-    assert torch.argmax(got) == torch.argmax(ref)
+    assert torch.argmax(got.cpu()) == torch.argmax(ref)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("steps", [1, 3])
+def test_fused_decode_matches_cpu_fp32_reference(steps):
+    """The decode path the e2e benchmark runs, checked against an independent reference: a
+    2-layer fuse=True model prefills 12 tokens, then decodes `steps` tokens one at a time, each
+    through the fused launches (int4_qkv_rope_cache with the RMSNorm prologue and the cache
+    writes, gate|up with RMSNorm, down with SwiGLU, the residual adds in o_proj and down).  The
+    logits of every decode step are compared with the CPU fp32 model (oracle W_hat) run over the
+    whole sequence so far (2e-2 rule, same argmax), and with a fuse=False model stepped the same
+    way (torch composition around int4_linear)."""
+    cfg = _small_cfg()
+    fused = tl.build_int4_model(cfg, DEV, seed=6, fuse=True)
+    plain = tl.build_int4_model(cfg, DEV, seed=6, fuse=False)
+    assert torch.equal(fused.layers[0].self_attn.q_proj.packed, plain.layers[0].self_attn.q_proj.packed)
+    assert all(ly.int4_fusable() and ly.self_attn.qkv is not None for ly in fused.layers)
+    ref_model = _cpu_fp32_reference(fused, cfg)
+    prompt = _prompt(12, cfg.vocab, seed=8)
+    rope = tl._rope_tables(cfg, DEV)
+    caches = {}
+    for name, model in (("fused", fused), ("plain", plain)):
+        caches[name] = model.new_cache(DEV)
+        pos = torch.arange(12, device=DEV)
+        model(prompt, pos, caches[name], rope, tl.causal_mask(pos, cfg.max_seq))
+    tokens = prompt.clone()
+    nxt = torch.from_numpy(np.random.default_rng(9).integers(0, cfg.vocab, steps)).to(DEV)
+    for i in range(steps):
+        tok = nxt[i:i + 1]
+        p1 = torch.tensor([12 + i], device=DEV)
+        got = {name: model(tok, p1, caches[name], rope, tl.causal_mask(p1, cfg.max_seq))
+               for name, model in (("fused", fused), ("plain", plain))}
+        tokens = torch.cat([tokens, tok])
+        ref = _cpu_logits(ref_model, cfg, tokens)
+        for name in ("fused", "plain"):
+            rel = _rel(got[name], ref)
+            assert rel < 2e-2, f"{name} decode step {i}: logits rel err {rel:.3e}"
+            assert torch.argmax(got[name].cpu()) == torch.argmax(ref), f"{name} decode step {i}: argmax"
+        assert _rel(got["fused"], got["plain"]) < 1e-2, f"fused vs unfused decode step {i}"
+
+
+@torch.no_grad()
+def test_graph_decoder_refuses_positions_past_the_cache():
+    """GraphDecoder keeps a host count of the position and raises before a step would write
+    past the history / cache (max_seq), instead of launching an out-of-range index."""
+    cfg = _small_cfg(layers=1, max_seq=24)
+    model = tl.build_int4_model(cfg, DEV, seed=4, fuse=True)
+    dec = tl.GraphDecoder(model, DEV)
+    dec.prefill(_prompt(16, cfg.vocab, seed=5))
+    dec.capture()
+    dec.decode(cfg.max_seq - 1 - 16)  # the last allowed step writes history[max_seq - 1]
+    with pytest.raises(ValueError, match="max_seq"):
+        dec.decode(1)
+    with pytest.raises(ValueError, match="max_seq"):
+        dec.prefill(_prompt(cfg.max_seq, cfg.vocab))
 
 
 @torch.no_grad()
