@@ -150,6 +150,22 @@ int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num
 int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y,
                  void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream);
 
+/* Bytes of split-K scratch kf_int4_gemm_noalloc holds per GPU (a device array in the library). */
+#define KF_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* kf_int4_gemm without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The split-K partials go to a device array of
+ * KF_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends;
+ * the call itself allocates nothing (no hipMalloc / hipFree).  Same plan, kernels and results
+ * as kf_int4_gemm, bit for bit.  A problem whose plan needs more partials than the scratch holds
+ * (kf_int4_gemm_workspace_bytes() > KF_NOALLOC_SCRATCH_BYTES) returns KF_ERR_WORKSPACE without
+ * launching.  All calls on one GPU share its scratch: calls that overlap on that GPU (other
+ * streams, other threads) race; serialize them.  The first call on a device looks up the scratch
+ * address (hipGetSymbolAddress) with that device current. */
+int kf_int4_gemm_noalloc(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
+                         int group_size, void* stream);
+
 /* MFMA-16 block copy of a packed weight (an internal layout; the public packed format is
  * unchanged): for every 16 rows of W and 128-k super-step, the 64 lanes' 16-byte pieces of
  * the MFMA fragments stored contiguously in lane order (lane l: row 16b + l%16, words

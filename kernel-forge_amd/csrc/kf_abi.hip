@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "kf_int4.h"
 #include "kf_launch.h"
@@ -81,9 +82,47 @@ int check_common(const void* x, const void* packed, const void* scales, const vo
   return KF_OK;
 }
 
-// kf_int4_gemm and kf_int4_gemm_mfma16: validation, plan, workspace check, launch.
+// ---- Scratch of kf_int4_gemm_noalloc --------------------------------------------------------
+// The split-K partials of the entry point that allocates nothing live in this file-scope device
+// array instead of a caller's workspace.  On the host, `scratch` names a host-side stand-in, not
+// a device address: host code never passes it to a kernel or a copy.  The device address of each
+// GPU's copy comes from hipGetSymbolAddress, called once per device with that device current
+// (scratch_ptr), and only that address is handed to the kernels.  Every call on a GPU shares the
+// GPU's copy, so calls that overlap on one GPU race; each call's split-K kernels overwrite every
+// element of the partials they later read, so nothing has to start at zero.
+constexpr size_t kScratchBytes = KF_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static_assert(kScratchBytes % 256 == 0, "scratch size");
+
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// Device address of the current device's scratch array, looked up on the first call per device.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(KF_ERR_HIP, "device ordinal %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess) return hip_status(err, "hipGetSymbolAddress(scratch)");
+      if (!p) return fail(KF_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address on device %d", dev);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return KF_OK;
+}
+
+// kf_int4_gemm, kf_int4_gemm_mfma16 and kf_int4_gemm_noalloc: validation, plan, workspace check,
+// launch.  With use_scratch the split-K partials go to this device's scratch array (ws is ignored).
 int gemm_entry(const void* x, const void* packed, const void* scales, const void* packed_r, const void* scales_r,
-               void* y, void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream) {
+               void* y, void* ws, size_t ws_bytes, int M, int N, int K, int group_size, void* stream,
+               bool use_scratch = false) {
 
   int st = check_common(x, packed, scales, y, M, N, K, group_size);
   if (st) return st;
@@ -98,7 +137,15 @@ int gemm_entry(const void* x, const void* packed, const void* scales, const void
     return fail(KF_ERR_UNSUPPORTED, "M=%d, N=%d exceed the grid limit for %dx%d tiles", M, N, plan.block_m,
                 plan.block_n);
   const size_t need = kf::gemm_workspace_bytes(plan, M, N);
-  if (need > 0) {
+  if (use_scratch) {
+    ws = nullptr;
+    if (need > kScratchBytes)
+      return fail(KF_ERR_WORKSPACE,
+                  "int4_gemm_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K partials, more than the %zu-byte "
+                  "scratch it holds; call kf_int4_gemm with a workspace",
+                  M, N, K, need, kScratchBytes);
+    if (need > 0 && (st = scratch_ptr(&ws))) return st;
+  } else if (need > 0) {
     if (!ws) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got NULL", need);
     if (ws_bytes < need) return fail(KF_ERR_WORKSPACE, "split-K workspace of %zu bytes required, got %zu", need, ws_bytes);
     if (!aligned(ws, 16)) return fail(KF_ERR_INVALID_ARG, "workspace must be 16-byte aligned");
@@ -243,6 +290,11 @@ int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num
 int kf_int4_gemm(const void* x, const void* packed, const void* scales, void* y, void* ws, size_t ws_bytes, int M,
                  int N, int K, int group_size, void* stream) {
   return gemm_entry(x, packed, scales, nullptr, nullptr, y, ws, ws_bytes, M, N, K, group_size, stream);
+}
+
+int kf_int4_gemm_noalloc(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
+                         int group_size, void* stream) {
+  return gemm_entry(x, packed, scales, nullptr, nullptr, y, nullptr, 0, M, N, K, group_size, stream, true);
 }
 
 int kf_int4_mfma16_sizes(int N, int K, int group_size, size_t* packed_bytes, size_t* scales_bytes) {

@@ -23,6 +23,7 @@ KF_PROLOGUE_NONE = 0
 KF_PROLOGUE_RMSNORM = 1
 KF_PROLOGUE_SWIGLU = 2
 KF_GEMV_FUSED_MAX_K = 10240
+KF_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 GEMV_MAX_GROUP = 8
 
@@ -55,6 +56,7 @@ SIGNATURES = {
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm_plan": (_I, [_I, _I, _I, _I, _IP, _IP, _IP, _IP, _IP]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
+    "kf_int4_gemm_noalloc": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "kf_int4_mfma16_sizes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "kf_int4_reorder_mfma16": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
     "kf_int4_gemm_mfma16": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
