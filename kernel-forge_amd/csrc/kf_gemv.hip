@@ -134,6 +134,19 @@ __device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane, 
 // Bytes of LDS one row of x takes (whole 1 KiB blocks, as the copy writes them).
 __device__ __forceinline__ uint32_t x_row_lds_bytes(int K) { return (uint32_t)((2 * K + 1023) & ~1023); }
 
+// Logical workgroup of this hardware workgroup.  The hardware deals workgroups to the 8 XCDs
+// round robin (workgroup b runs on XCD b % 8); the logical ids give each XCD runs of kXcdRun
+// consecutive workgroups, so consecutive rows - and each 128-byte line of y they store - stay
+// in one XCD's L2 (7 TinyLlama linears at M = 1: 5.73 -> 5.66 us, Qwen2.5: 7.05 -> 6.85 us on
+// MI355X; every problem still spreads evenly over the XCDs).  Launches pad their grid to whole
+// runs of all XCDs (kXcdGrid workgroups); padded workgroups get ids past the real ones.
+constexpr int kXcdRun = 8;
+constexpr int kXcdGrid = 8 * kXcdRun;
+__device__ __forceinline__ int xcd_run_block() {
+  const int hb = blockIdx.x, j = hb >> 3;
+  return (j / kXcdRun) * kXcdGrid + (hb & 7) * kXcdRun + (j % kXcdRun);
+}
+
 // Sum over the 64 lanes, returned to every lane: lanes i and i + 32 paired by permlane32_swap,
 // then the DPP half-wave sum, read from lane 31.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -302,7 +315,9 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
   // With x in LDS, the chunk sums of x need nothing from the weight loads: computed here, ahead
   // of the first weight use, they run while those loads are in flight instead of after the
   // wait for them (same operations in the same order, so the same bits).  M <= 2 only: above
-  // that the extra live sums cost occupancy in the unrolled kernels.
+  // that the extra live sums cost occupancy in the unrolled kernels.  (A table of the sums
+  // built once per workgroup in LDS does 4x less VALU work but costs a second barrier, and
+  // measured slower: 7 TinyLlama linears 5.72 -> 5.79 us.)
   constexpr bool kEarlyXsum = XLDS && M <= 2;
   float xs8_early[UU][XM];
   if constexpr (kEarlyXsum) {
@@ -463,7 +478,9 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const hal
                                                                      half_t* __restrict__ y, int N, int K,
                                                                      int scale_shift) {
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  const int lb = xcd_run_block();
+  if (lb * kGemvWavesPerBlock * R >= N) return;  // a padded workgroup: all of its wavefronts leave
+  const int row0 = (lb * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
   if (!XLDS && row0 >= N) return;  // past the last row
   gemv_rows<M, R, UMAX, XLDS>(x, packed, scales, y, N, K, scale_shift, row0, lane);
 }
@@ -475,7 +492,9 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_fused_kernel(
     const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
     int N, int K, int scale_shift, const half_t* res, const half_t* __restrict__ aux, float eps) {
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  const int lb = xcd_run_block();
+  if (lb * kGemvWavesPerBlock * R >= N) return;  // a padded workgroup: all of its wavefronts leave
+  const int row0 = (lb * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
   gemv_rows<1, R, UMAX, true, PRO>(x, packed, scales, y, N, K, scale_shift, row0, lane, res, aux, eps);
 }
 
@@ -487,7 +506,9 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_qkv_rope_kernel(
     const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
     int N, int K, int scale_shift, const half_t* __restrict__ aux, float eps, const GemvRope rope) {
   const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lb = xcd_run_block();
+  if (lb * kGemvWavesPerBlock * 2 >= N) return;  // a padded workgroup: all of its wavefronts leave
+  const int w = lb * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half_d = rope.head_dim >> 1;
   const int nwr = (rope.heads + rope.kv_heads) * half_d;
   int row0, step;
@@ -516,8 +537,9 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(i
                                                                              int b7, int b8,
                                                                              const GemvTable table) {
   const int lane = threadIdx.x & 63;
-  const int gwave = blockIdx.x * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // gwave - b >> 31 is 1 exactly when gwave < b (both in [0, 2^31)).
+  const int gwave = xcd_run_block() * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // gwave - b >> 31 is 1 exactly when gwave < b (both in [0, 2^31)); padded workgroups lie past
+  // the last problem's waves.
   const unsigned g = (unsigned)gwave;
   const int p = kMaxGemvGroup - (int)(((g - b1) >> 31) + ((g - b2) >> 31) + ((g - b3) >> 31) + ((g - b4) >> 31) +
                                       ((g - b5) >> 31) + ((g - b6) >> 31) + ((g - b7) >> 31) + ((g - b8) >> 31));
@@ -612,6 +634,9 @@ void* pick(int M, const GemvPlan& plan) {
 
 // Dynamic LDS of the x copy: whole 1 KiB blocks of M * K fp16 values.
 size_t x_lds_bytes(int M, int K) { return (size_t)ceil_div(M * K * 2, 1024) * 1024; }
+
+// A grid of `blocks` workgroups padded to whole XCD runs (see xcd_run_block).
+int xcd_grid(int blocks) { return ceil_div(blocks, kXcdGrid) * kXcdGrid; }
 
 typedef void (*GemvFusedFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int, const half_t*,
                             const half_t*, float);
@@ -719,7 +744,7 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
   const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
   if (count == 1) {
     const GemvProblem& q = problems[0];
-    const int blocks = ceil_div(ceil_div(q.N, plan.rows_per_wave), kGemvWavesPerBlock);
+    const int blocks = xcd_grid(ceil_div(ceil_div(q.N, plan.rows_per_wave), kGemvWavesPerBlock));
     const size_t lds = plan.x_lds ? x_lds_bytes(M, q.K) : 0;
     hipLaunchKernelGGL(reinterpret_cast<GemvFn>(pick<false>(M, plan)), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
                        lds, stream, static_cast<const half_t*>(q.x), static_cast<const uint32_t*>(q.packed),
@@ -753,7 +778,7 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
       bounds[i] = INT_MAX;
     }
   }
-  const int blocks = ceil_div(waves, kGemvWavesPerBlock);
+  const int blocks = xcd_grid(ceil_div(waves, kGemvWavesPerBlock));
   const size_t lds = plan.x_lds ? x_lds_bytes(M, max_k) : 0;
   hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(pick<true>(M, plan)), dim3(blocks),
                      dim3(64 * kGemvWavesPerBlock), lds, stream, count, shift, bounds[0], bounds[1], bounds[2],
@@ -764,7 +789,7 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
 hipError_t gemv_qkv_rope_launch(const GemvProblem& q, const GemvFused& f, const GemvRope& rope, int unroll,
                                 int group_size, hipStream_t stream) {
   const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
-  const int blocks = ceil_div(ceil_div(q.N, 2), kGemvWavesPerBlock);
+  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, 2), kGemvWavesPerBlock));
   const GemvRopeFn fn = f.prologue == kGemvProRmsNorm ? pick_rope_u<kGemvProRmsNorm>(unroll)
                                                       : pick_rope_u<kGemvProNone>(unroll);
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * kGemvWavesPerBlock), fused_lds_bytes(q.K, f.prologue), stream,
@@ -783,7 +808,7 @@ hipError_t gemv_fused_launch(const GemvPlan& plan, const GemvProblem& q, const G
   // third row's sums are added in the same order, so the bits do not change.
   int rows = plan.rows_per_wave == 1 ? 1 : 2;
   if (rows == 2 && f.prologue != kGemvProNone && q.N >= 8192) rows = 3;
-  const int blocks = ceil_div(ceil_div(q.N, rows), kGemvWavesPerBlock);
+  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, rows), kGemvWavesPerBlock));
   hipLaunchKernelGGL(pick_fused(f.prologue, rows, plan.unroll), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
                      fused_lds_bytes(q.K, f.prologue), stream, static_cast<const half_t*>(q.x),
                      static_cast<const uint32_t*>(q.packed), static_cast<const half_t*>(q.scales),
