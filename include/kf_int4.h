@@ -215,6 +215,13 @@ int kf_bw_copy(const void* src, void* dst, size_t bytes, int grid_blocks, void* 
 int kf_bw_read(const void* src, void* sink, size_t bytes, int grid_blocks, void* stream);
 int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream);
 
+/* kf_bw_read that also stores, as a decode GEMV does: 2 fp16 values per wavefront of 64 threads
+ * (lanes 31 and 63) into out, adjacent across wavefronts, so out needs 16 * grid_blocks bytes.
+ * The same-size read with and without these stores bounds what a one-launch GEMV step that must
+ * write its outputs can reach.  No reference counterpart (a measurement kernel beside
+ * csrc/micro/bandwidth.cu:17-42's). */
+int kf_bw_read_store(const void* src, void* out, size_t bytes, int grid_blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

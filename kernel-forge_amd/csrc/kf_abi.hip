@@ -388,6 +388,14 @@ int kf_bw_read(const void* src, void* sink, size_t bytes, int grid_blocks, void*
   return hip_status(kf::bw_read_launch(src, sink, bytes, grid_blocks, static_cast<hipStream_t>(stream)), "bw_read");
 }
 
+int kf_bw_read_store(const void* src, void* out, size_t bytes, int grid_blocks, void* stream) {
+  int st = bw_args(src, bytes, &grid_blocks);
+  if (st) return st;
+  if (!out || !aligned(out, 2)) return fail(KF_ERR_INVALID_ARG, "out must be non-null and 2-byte aligned");
+  return hip_status(kf::bw_read_store_launch(src, out, bytes, grid_blocks, static_cast<hipStream_t>(stream)),
+                    "bw_read_store");
+}
+
 int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream) {
   int st = bw_args(dst, bytes, &grid_blocks);
   if (st) return st;

@@ -41,6 +41,19 @@ __global__ __launch_bounds__(256) void bw_read_kernel(const u32x4* __restrict__ 
   if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
 }
 
+// bw_read_kernel plus the stores of a decode GEMV: lanes 31 and 63 of every wavefront store one
+// fp16 each (2 bytes, 4 per wavefront, wavefronts' values adjacent), unconditionally, so the
+// kernel ends with the small scattered stores the GEMV's outputs make.
+__global__ __launch_bounds__(256) void bw_read_store_kernel(const u32x4* __restrict__ src, uint16_t* __restrict__ out,
+                                                             size_t n) {
+  uint32_t acc = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const u32x4 v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if ((threadIdx.x & 31) == 31) out[((size_t)blockIdx.x * 256 + threadIdx.x) >> 5] = (uint16_t)acc;
+}
+
 __global__ __launch_bounds__(256) void bw_write_kernel(u32x4* __restrict__ dst, size_t n) {
   const u32x4 v = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
@@ -69,6 +82,12 @@ hipError_t bw_copy_launch(const void* src, void* dst, size_t bytes, int grid, hi
 hipError_t bw_read_launch(const void* src, void* sink, size_t bytes, int grid, hipStream_t stream) {
   hipLaunchKernelGGL(bw_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(src),
                      static_cast<uint32_t*>(sink), bytes / 16);
+  return hipGetLastError();
+}
+
+hipError_t bw_read_store_launch(const void* src, void* out, size_t bytes, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(bw_read_store_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(src),
+                     static_cast<uint16_t*>(out), bytes / 16);
   return hipGetLastError();
 }
 

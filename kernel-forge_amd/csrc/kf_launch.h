@@ -143,6 +143,7 @@ hipError_t dequant_fp16_launch(const void* packed, const void* scales, void* w_h
                                hipStream_t stream);
 hipError_t bw_copy_launch(const void* src, void* dst, size_t bytes, int grid, hipStream_t stream);
 hipError_t bw_read_launch(const void* src, void* sink, size_t bytes, int grid, hipStream_t stream);
+hipError_t bw_read_store_launch(const void* src, void* out, size_t bytes, int grid, hipStream_t stream);
 hipError_t bw_write_launch(void* dst, size_t bytes, int grid, hipStream_t stream);
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }

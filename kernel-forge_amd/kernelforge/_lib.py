@@ -65,6 +65,7 @@ SIGNATURES = {
     "kf_bw_copy": (_I, [_VP, _VP, _SZ, _I, _VP]),
     "kf_bw_read": (_I, [_VP, _VP, _SZ, _I, _VP]),
     "kf_bw_write": (_I, [_VP, _SZ, _I, _VP]),
+    "kf_bw_read_store": (_I, [_VP, _VP, _SZ, _I, _VP]),
 }
 
 _lib: ctypes.CDLL | None = None
