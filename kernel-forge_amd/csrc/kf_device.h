@@ -99,6 +99,24 @@ __device__ __forceinline__ float half_sum_lanes31_63(float v) {
   return v;
 }
 
+// Waits until at most N vector-memory operations of this wavefront are outstanding.  LDS-DMA
+// copies (global_load_lds_*) are issued from inline assembly, which the compiler neither tracks
+// nor orders against its own waits, so the kernels wait for a copy with a counted wait: N is the
+// number of vector-memory instructions the kernel issues after that copy (the GEMV's first-pass
+// weight and scale loads; the GEMM's next stage of DMAs).  That count holds only while the
+// compiler emits exactly those instructions in between; a different count would let a wavefront
+// read LDS before its copy lands.  Built with KF_DMA_WAIT_ALL defined (KF_DMA_WAIT_ALL=1 in the
+// environment of kernelforge/build.py), every such wait is vmcnt(0) instead: slower, and
+// correct whatever the compiler emits.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+#ifdef KF_DMA_WAIT_ALL
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#else
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#endif
+}
+
 __device__ __forceinline__ u32x4 load_u32x4(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

@@ -508,9 +508,9 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   };
   auto wait_older = [&](bool newer_has_scales) {  // all but the newest stage's loads landed
     if (newer_has_scales)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerStage + 1) : "memory");
+      wait_vmcnt<kDmaPerStage + 1>();
     else
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerStage) : "memory");
+      wait_vmcnt<kDmaPerStage>();
   };
 
   float4_t acc[TM][TN];

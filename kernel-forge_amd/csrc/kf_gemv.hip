@@ -298,7 +298,7 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
   }
   if constexpr (XLDS) {
     if (first) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * UU * R) : "memory");
+      wait_vmcnt<2 * UU * R>();
       __syncthreads();
       if constexpr (PRO != kGemvProNone) x_prologue<PRO>(rs.K, rs.eps);
     }

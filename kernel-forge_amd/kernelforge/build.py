@@ -38,6 +38,13 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result"]
 
 
+def device_flags() -> list[str]:
+    """DEVICE_FLAGS, plus -DKF_DMA_WAIT_ALL when KF_DMA_WAIT_ALL=1 is set: every counted wait for
+    an LDS-DMA copy becomes a wait for all outstanding vector-memory operations (kf_device.h)."""
+    extra = ["-DKF_DMA_WAIT_ALL"] if os.environ.get("KF_DMA_WAIT_ALL", "0") not in ("", "0") else []
+    return DEVICE_FLAGS + extra
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -86,7 +93,7 @@ def build_library(verbose: bool = False, resource_usage: bool = False) -> Path:
 
     def compile_one(src: str) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
-        cmd = [cc, *COMMON_FLAGS, *DEVICE_FLAGS, *extra, "-I", str(INCLUDE_DIR), "-I", str(SRC_DIR),
+        cmd = [cc, *COMMON_FLAGS, *device_flags(), *extra, "-I", str(INCLUDE_DIR), "-I", str(SRC_DIR),
                "-c", str(SRC_DIR / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))

@@ -20,3 +20,13 @@ x.hip:9:1: remark:     ScratchSize [bytes/lane]: 576 [-Rpass-analysis=kernel-res
     spill = ok.replace("VGPRs Spill: 0", "VGPRs Spill: 12")
     with pytest.raises(RuntimeError, match="k_ok: VGPRs Spill = 12"):
         build._check_resources(spill, "x.hip")
+
+
+def test_dma_wait_all_switch(monkeypatch):
+    """KF_DMA_WAIT_ALL=1 adds the define that turns every counted LDS-DMA wait into vmcnt(0)."""
+    monkeypatch.delenv("KF_DMA_WAIT_ALL", raising=False)
+    assert "-DKF_DMA_WAIT_ALL" not in build.device_flags()
+    monkeypatch.setenv("KF_DMA_WAIT_ALL", "1")
+    assert "-DKF_DMA_WAIT_ALL" in build.device_flags()
+    monkeypatch.setenv("KF_DMA_WAIT_ALL", "0")
+    assert "-DKF_DMA_WAIT_ALL" not in build.device_flags()
