@@ -327,7 +327,7 @@ def int4_dequant_fp16(packed: torch.Tensor, scales: torch.Tensor, group_size: in
 
 
 def int4_gemv_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
-                      group_size: int = 128) -> list[torch.Tensor]:
+                      group_size: int = 128, *, _checked: bool = False) -> list[torch.Tensor]:
     """Several independent INT4 GEMVs (common M in [1, 8]) in one kernel launch per 8 problems.
 
     Each output equals ``int4_gemv(xs[i], packed[i], scales[i], group_size)`` bit for bit.
@@ -340,7 +340,8 @@ def int4_gemv_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales
         raise ValueError("xs, packed and scales must be non-empty lists of equal length")
     m = xs[0].shape[0] if isinstance(xs[0], torch.Tensor) and xs[0].dim() == 2 else -1
     for x, p, s in zip(xs, packed, scales):
-        _check_int4(x, p, s, group_size)
+        if not _checked:
+            _check_int4(x, p, s, group_size)
         if x.shape[0] != m:
             raise ValueError(f"all problems must share M, got {x.shape[0]} and {m}")
         if x.device != xs[0].device:
@@ -354,11 +355,14 @@ def int4_gemv_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales
     with _on(dev):
         stream = _stream_ptr(dev)
         for b0 in range(0, len(xs), _lib.GEMV_MAX_GROUP):
-            idx = range(b0, min(b0 + _lib.GEMV_MAX_GROUP, len(xs)))
-            probs = (_lib.GemvProblem * len(idx))(*[
-                _lib.GemvProblem(_ptr(xs[i]), _ptr(packed[i]), _ptr(scales[i]), _ptr(ys[i]),
-                                 packed[i].shape[0], xs[i].shape[1]) for i in idx])
-            status = lib.kf_int4_gemv_grouped(probs, len(idx), m, int(group_size), stream)
+            b1 = min(b0 + _lib.GEMV_MAX_GROUP, len(xs))
+            probs = (_lib.GemvProblem * (b1 - b0))()
+            for j, i in enumerate(range(b0, b1)):
+                pr = probs[j]
+                pr.x, pr.packed, pr.scales, pr.y = (xs[i].data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(),
+                                                    ys[i].data_ptr())
+                pr.N, pr.K = packed[i].shape[0], xs[i].shape[1]
+            status = lib.kf_int4_gemv_grouped(probs, b1 - b0, m, int(group_size), stream)
             _lib.check(status, "int4_gemv_grouped")
     return ys
 
@@ -374,9 +378,10 @@ def _(x, packed, scales, group_size):
 
 
 def _matmul_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales: list[torch.Tensor],
-                    group_size: int) -> list[torch.Tensor]:
+                    group_size: int, checked: bool = False) -> list[torch.Tensor]:
+    """checked: _check_int4 has passed on every problem (int4_linear_grouped's eager path)."""
     if all(_use_gemv(x.shape[0], p.shape[0]) for x, p in zip(xs, packed)):
-        return int4_gemv_grouped(xs, packed, scales, group_size)
+        return int4_gemv_grouped(xs, packed, scales, group_size, _checked=checked)
     if xs[0].shape[0] <= _GEMV_LIMIT_M:
         return [int4_matmul(x, p, s, group_size) for x, p, s in zip(xs, packed, scales)]
     return [int4_gemm(x, p, s, group_size) for x, p, s in zip(xs, packed, scales)]
@@ -398,23 +403,22 @@ def int4_linear_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scal
                         ) -> list[torch.Tensor]:
     """``[int4_linear(xs[i], packed[i], scales[i], group_size, biases[i]) ...]`` with one GEMV launch
     for all problems at decode sizes (common flattened M <= GEMV_MAX_M); results are bit-identical."""
-    leads, flat = [], []
+    flat = []
     for x in xs:
-        leads.append(x.shape[:-1])
-        x2 = x.reshape(-1, x.shape[-1])
+        x2 = x if x.dim() == 2 else x.reshape(-1, x.shape[-1])
         flat.append(x2 if x2.is_contiguous() else x2.contiguous())
     for x2, p, s in zip(flat, packed, scales):
         _check_int4(x2, p, s, group_size)
     if torch.compiler.is_compiling():
         ys = _int4_matmul_grouped_op(flat, list(packed), list(scales), int(group_size))
-    else:  # eager: the op's implementation without the dispatcher (as in int4_linear)
-        ys = _matmul_grouped(flat, list(packed), list(scales), int(group_size))
+    else:  # eager: the op's implementation without the dispatcher (as in int4_linear), checked once
+        ys = _matmul_grouped(flat, list(packed), list(scales), int(group_size), checked=True)
     out = []
     for i, y in enumerate(ys):
         b = biases[i] if biases is not None else None
         if b is not None:
             y = y + b
-        out.append(y.reshape(*leads[i], packed[i].shape[0]))
+        out.append(y if xs[i].dim() == 2 else y.reshape(*xs[i].shape[:-1], packed[i].shape[0]))
     return out
 
 
