@@ -305,7 +305,9 @@ class GraphSteps:
         return [self.copies] * full + ([rem] if rem else [])
 
     def prepare(self, count: int) -> None:
-        """Captures every graph run(count) replays."""
+        """Captures every graph run(count) replays, and replays each new one once: a graph's first
+        launch also does one-time work (its kernel arguments are uploaded to the device), which
+        must not land in a timed run."""
         for n in set(self._sizes(count)):
             if n not in self.graphs:
                 g = self.torch.cuda.CUDAGraph()
@@ -313,6 +315,7 @@ class GraphSteps:
                     for r in range(n):
                         self.step_fn(r)
                 self.graphs[n] = g
+                g.replay()
         self.torch.cuda.synchronize()
 
     def run(self, count: int) -> None:
