@@ -84,6 +84,23 @@ typedef struct kf_gemv_problem {
  * the time to stream a whole small layer. */
 int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int group_size, void* stream);
 
+/* The launch plan of kf_int4_gemv (count = 1) or kf_int4_gemv_grouped for these shapes, on a
+ * GPU with cu_count compute units (<= 0: the current device's).  *kernel: KF_GEMV_KERNEL_*;
+ * rows[i] (count entries): output rows per wavefront of problem i (1, 2 or 3), KF_GEMV_FLAT + F
+ * (F rows of K = 1024 or 1536 per wavefront, their chunks packed into full 64-lane loads) or
+ * KF_GEMV_DEEP (one row per wavefront, up to four 64-chunk blocks per memory round trip);
+ * *unroll: 64-chunk blocks per pass of the other rows; *x_lds: 1 when each workgroup stages x in
+ * LDS.  Any output pointer may be NULL.  Host code only (no launch, no device access when
+ * cu_count > 0).  For diagnostics and tests; no reference counterpart. */
+#define KF_GEMV_KERNEL_ROWS1 1   /* one row per wavefront */
+#define KF_GEMV_KERNEL_ROWS2 2   /* two rows per wavefront */
+#define KF_GEMV_KERNEL_MIXED 3   /* grouped: two or three rows per problem */
+#define KF_GEMV_KERNEL_SHAPED 4  /* grouped, M = 1: also flat and deep rows */
+#define KF_GEMV_DEEP 8
+#define KF_GEMV_FLAT 16
+int kf_int4_gemv_plan(int M, const int* N, const int* K, int count, int cu_count, int* kernel, int* rows,
+                      int* unroll, int* x_lds);
+
 #define KF_PROLOGUE_NONE 0     /* x as given */
 #define KF_PROLOGUE_RMSNORM 1  /* x * rsqrt(mean(x^2) + eps) * aux, aux = fp16 norm weight [K] */
 #define KF_PROLOGUE_SWIGLU 2   /* fp16(fp16(silu(x)) * aux): x = gate [K], aux = up [K] */

@@ -204,6 +204,33 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
                     "int4_gemv_grouped launch");
 }
 
+int kf_int4_gemv_plan(int M, const int* N, const int* K, int count, int cus_given, int* kernel, int* rows,
+                      int* unroll, int* x_lds) {
+  static_assert(KF_GEMV_FLAT == kf::kGemvFlat && KF_GEMV_DEEP == kf::kGemvDeep &&
+                    KF_GEMV_KERNEL_MIXED == kf::kGemvRowsMixed && KF_GEMV_KERNEL_SHAPED == kf::kGemvRowsShaped,
+                "plan codes");
+  if (!N || !K) return fail(KF_ERR_INVALID_ARG, "N and K must be non-null");
+  if (count < 1 || count > KF_GEMV_MAX_GROUP)
+    return fail(KF_ERR_INVALID_ARG, "count must be in [1, %d], got %d", KF_GEMV_MAX_GROUP, count);
+  if (M < 1 || M > 8) return fail(KF_ERR_INVALID_ARG, "int4_gemv handles M in [1, 8], got M=%d", M);
+  for (int i = 0; i < count; ++i)
+    if (N[i] < 1 || K[i] < 64 || K[i] % 64)
+      return fail(KF_ERR_INVALID_ARG, "problem %d: N >= 1 and K a positive multiple of 64, got N=%d K=%d", i, N[i],
+                  K[i]);
+  int cus = cus_given;
+  if (cus <= 0) {
+    const int st = cu_count(&cus);
+    if (st) return st;
+  }
+  const kf::GemvPlan p = kf::gemv_plan(M, N, K, count, cus);
+  if (kernel) *kernel = p.rows_per_wave;
+  if (rows)
+    for (int i = 0; i < count; ++i) rows[i] = p.rows[i];
+  if (unroll) *unroll = p.unroll;
+  if (x_lds) *x_lds = p.x_lds ? 1 : 0;
+  return KF_OK;
+}
+
 int kf_int4_gemv_fused(const void* x, const void* packed, const void* scales, void* y, int M, int N, int K,
                        int group_size, int prologue, const void* aux, float eps, const void* residual, void* stream) {
   int st = check_common(x, packed, scales, y, M, N, K, group_size);

@@ -27,7 +27,11 @@
 //   * Each wavefront owns R consecutive rows of one problem (R = 1 or 2; a
 //     grouped launch that would not fit one resident round gives its largest
 //     problems 3).  Lane l handles chunks l, l+64, ... of its rows, so a
-//     wavefront-wide dwordx4 streams 1 KiB of a row contiguously.
+//     wavefront-wide dwordx4 streams 1 KiB of a row contiguously.  Large
+//     grouped launches at M = 1 also use flat rows (K = 1024 / 1536: several
+//     short rows per full load, gemv_rows_flat) and deep rows (one long row,
+//     up to four blocks per round trip, gemv_row_deep); both give every row the
+//     bits gemv_rows gives it.
 //   * A pass covers UU (1..4) consecutive 64-chunk blocks; UU is picked per
 //     pass from the chunks left in the row, so a K=5632 row is one pass of
 //     3 blocks and a K=2048 row one pass of 1, in the same launch.  Every load
@@ -468,6 +472,190 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
   }
 }
 
+// Flat rows (M = 1, x in LDS): rows of C = K / 32 < 64 chunks, E = 64 - C dividing C
+// (gemv_flat_rows).  The wavefront owns F = L + 1 rows row0 .. row0 + L, L = C / E, and issues L
+// full 64-lane loads: load j holds row row0 + j in lanes 0 .. C - 1 (chunk = lane, as in
+// gemv_rows) and chunks E j .. E j + E - 1 of the last row in lanes C .. 63.  Every lane computes
+// fmaf(s, dot, 0) per chunk, the value gemv_rows' single pass leaves in that chunk's lane; the
+// last row's values are then moved to lane = chunk (ds_bpermute) and each row is reduced with
+// gemv_rows' two-row tree, so a row's result has the same bits as in gemv_rows.  A wavefront
+// thus moves 1 KiB per load instead of 2 C * 8 bytes, and a K = 1536 problem needs a quarter
+// fewer wavefronts than at three rows each.  Rows past N are clamped for loading, never stored.
+template <int C>
+__device__ __forceinline__ void gemv_rows_flat(const half_t* x, const uint32_t* packed, const half_t* scales,
+                                               half_t* y, int N, int scale_shift, int row0, int lane) {
+  constexpr int E = 64 - C, L = C / E, F = L + 1, K = 32 * C;
+  static_assert(E * L == C && F % 2 == 0 && L <= 3 && (E & (E - 1)) == 0, "flat rows: E, a power of two, divides C");
+  stage_x_lds(x, K >> 3, lane);
+  // As in gemv_rows: the weight and scale bases pass through an opaque move so their loads
+  // stay after the copy, which the wait below counts on.
+  uintptr_t pa = (uintptr_t)packed, sa = (uintptr_t)scales;
+  asm volatile("" : "+s"(pa), "+s"(sa));
+  const char* pk = (const char*)(const __attribute__((address_space(1))) char*)pa;
+  const char* sc = (const char*)(const __attribute__((address_space(1))) char*)sa;
+
+  const bool extra = lane >= C;  // lanes carrying the last row
+  const int ce = lane - C;       // their chunk offset within each load's E chunks
+  const size_t srow_bytes = (size_t)(C >> scale_shift) * 2;
+  const int nlast = min(row0 + L, N - 1);
+  u32x4 wv[L];
+  half_t sv[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const size_t n = (size_t)(extra ? nlast : min(row0 + j, N - 1));
+    const uint32_t c = (uint32_t)(extra ? E * j + ce : lane);
+    wv[j] = load_u32x4_stream(pk + n * (16 * C) + 16u * c);
+    sv[j] = *reinterpret_cast<const half_t*>(sc + n * srow_bytes + 2u * (c >> scale_shift));
+  }
+  wait_vmcnt<2 * L>();  // the x copy has landed (only this wavefront's 2 L loads follow it)
+  __syncthreads();
+
+  // x of a lane's chunk: lanes below C see chunk `lane` in every load, the extra lanes chunk
+  // E j + ce of load j, read into the same registers under their own mask.
+  u32x4 xm[4];
+  {
+    const int xi = 4 * (extra ? ce : lane);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xm[q] = gemv_x_lds[xi + q];
+  }
+  // Chunk sums: lane t < C sums chunk t, once; in load j > 0 the extra lanes take the sum of
+  // their chunk E j + ce from lane E j + ce (the same value, fetched instead of recomputed:
+  // Qwen2.5's 7 linears 6.57 -> 6.39 us on MI355X).
+  const float xs_own = chunk_xsum(xm) * kMinus8TwoPowMinus24;
+  float prod[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    float xs8 = xs_own;
+    if (j > 0) {
+      const float moved =
+          __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (E * j + (ce & (E - 1))), __float_as_int(xs_own)));
+      if (extra) {
+        xs8 = moved;
+        const int xi = 4 * (E * j + ce);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xm[q] = gemv_x_lds[xi + q];
+      }
+    }
+    ChunkNibbles nb;
+    split_chunk(wv[j], nb);
+    prod[j] = fmaf((float)sv[j], chunk_dot(nb, xm, xs8), 0.0f);
+  }
+
+  // Row values in chunk order: rows 0 .. L - 1 in lanes 0 .. C - 1 as loaded; the last row's
+  // chunk t comes from load t / E, lane C + t % E.  Lanes C .. 63 hold 0 for every row, as the
+  // lanes past a row's chunks do in gemv_rows.
+  float v[F];
+#pragma unroll
+  for (int j = 0; j < L; ++j) v[j] = extra ? 0.0f : prod[j];
+  {
+    const int src = 4 * (C + lane % E);
+    const int jl = lane / E;
+    float last = 0.0f;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const float moved = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(prod[j])));
+      if (jl == j) last = moved;
+    }
+    v[L] = extra ? 0.0f : last;
+  }
+#pragma unroll
+  for (int p = 0; p < F / 2; ++p) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * p]), __float_as_uint(v[2 * p + 1]),
+                                                     false, false);
+    const float tot = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+    const int n = row0 + 2 * p + (lane >> 5);
+    if ((lane & 31) == 31 && n < N) y[n] = (half_t)(tot * kTwoPow24);
+  }
+}
+
+// One pass of gemv_row_deep: UU blocks of one row, every weight and scale load issued first,
+// then per block its x chunk read from LDS, its chunk sum and its product.  Values and order
+// are gemv_pass's for R = 1, M = 1: lane l adds chunk l + 64 u of the pass after chunk
+// l + 64 (u - 1), each as fmaf(s, dot, acc).
+template <int UU>
+__device__ __forceinline__ void gemv_deep_pass(const char* prow, const char* srow, int chunks, int scale_shift,
+                                               int cb, int lane, float& acc, bool first) {
+  u32x4 wv[UU];
+  half_t sv[UU];
+#pragma unroll
+  for (int u = 0; u < UU; ++u) {
+    const uint32_t c = (uint32_t)min(cb + lane + 64 * u, chunks - 1);
+    wv[u] = load_u32x4_stream(prow + 16u * c);
+    sv[u] = *reinterpret_cast<const half_t*>(srow + 2u * (c >> scale_shift));
+  }
+  if (first) {
+    wait_vmcnt<2 * UU>();  // the x copy has landed (only this pass's 2 UU loads follow it)
+    __syncthreads();
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load of the pass ahead of the math
+#pragma unroll
+  for (int u = 0; u < UU; ++u) {
+    const int c = cb + lane + 64 * u;
+    const int xi = 4 * min(c, chunks - 1);
+    u32x4 xm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xm[q] = gemv_x_lds[xi + q];
+    const float xs8 = chunk_xsum(xm) * kMinus8TwoPowMinus24;
+    // Every lane computes (past the row's end on its clamped chunk) and keeps the sum only in
+    // range: a branch here would let a pass end with loads never waited for, and the compiler
+    // would then wait for all loads, the x copy included, before the next pass's first weights.
+    ChunkNibbles nb;
+    split_chunk(wv[u], nb);
+    const float next = fmaf((float)sv[u], chunk_dot(nb, xm, xs8), acc);
+    acc = c < chunks ? next : acc;
+  }
+}
+
+// One pass of gemv_row_deep from chunk cb with as many blocks (up to UMAX) as the row has left;
+// returns the next pass's first chunk.
+template <int UMAX>
+__device__ __forceinline__ int gemv_deep_passes(const char* prow, const char* srow, int chunks, int scale_shift,
+                                                int cb, int lane, float& acc, bool first) {
+  const int left = chunks - cb;  // uniform
+  if (UMAX >= 4 && left > 192) {
+    gemv_deep_pass<(UMAX >= 4 ? 4 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
+    return cb + 256;
+  }
+  if (UMAX >= 3 && left > 128) {
+    gemv_deep_pass<(UMAX >= 3 ? 3 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
+    return cb + 192;
+  }
+  if (UMAX >= 2 && left > 64) {
+    gemv_deep_pass<(UMAX >= 2 ? 2 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
+    return cb + 128;
+  }
+  gemv_deep_pass<1>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
+  return cb + 64;
+}
+
+// Deep rows (M = 1, x in LDS): one row per wavefront, up to UMAX 64-chunk blocks per memory
+// round trip.  A pass holds its weights and scales (5 registers per block) and one chunk of
+// x at a time, so three blocks per pass fit the register budget of a full-occupancy launch
+// (gemv_rows keeps every block's x of a pass in registers).  Chunks, products, their order and
+// the one-row reduction are gemv_rows' for R = 1, so the row has the same bits as there.
+template <int UMAX>
+__device__ __forceinline__ void gemv_row_deep(const half_t* x, const uint32_t* packed, const half_t* scales,
+                                              half_t* y, int N, int K, int scale_shift, int row, int lane) {
+  stage_x_lds(x, K >> 3, lane);
+  uintptr_t pa = (uintptr_t)packed, sa = (uintptr_t)scales;  // see gemv_rows
+  asm volatile("" : "+s"(pa), "+s"(sa));
+  const char* pk = (const char*)(const __attribute__((address_space(1))) char*)pa;
+  const char* sc = (const char*)(const __attribute__((address_space(1))) char*)sa;
+  const int chunks = K >> 5;
+  const size_t n = (size_t)min(row, N - 1);
+  const char* prow = pk + n * (size_t)(K >> 1);
+  const char* srow = sc + n * (size_t)((chunks >> scale_shift) * 2);
+  // The first pass always spans UMAX blocks (blocks past the row's end load its last chunk and
+  // add nothing): one code path from the x copy to the first weights, so the compiler's wait
+  // analysis sees no other pass's loads before them and does not wait for the copy.
+  float acc = 0.0f;
+  gemv_deep_pass<UMAX>(prow, srow, chunks, scale_shift, 0, lane, acc, true);
+  for (int cb = 64 * UMAX; cb < chunks;) cb = gemv_deep_passes<UMAX>(prow, srow, chunks, scale_shift, cb, lane, acc, false);
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+  const float tot = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+  if (lane == 31 && row < N) y[row] = (half_t)(tot * kTwoPow24);
+}
+
 // One problem: every argument is a scalar kernel argument, preloaded into SGPRs, so a
 // wavefront issues its weight loads without waiting on any scalar memory access.  With
 // XLDS every wavefront takes part in the x copy and its barrier, so none leaves early.
@@ -555,8 +743,26 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(i
   typedef const __attribute__((address_space(1))) half_t* gh_t;
   typedef const __attribute__((address_space(1))) uint32_t* gu_t;
   typedef __attribute__((address_space(1))) half_t* gy_t;
-  if constexpr (R == kGemvRowsMixed) {
-    // Mixed launch: each problem carries its own rows per wavefront (2 or 3) in the slot.
+  if constexpr (R == kGemvRowsMixed || R == kGemvRowsShaped) {
+    // Mixed launch: each problem carries its own rows per wavefront (2 or 3; in the shaped
+    // launch also flat or deep rows) in the slot.
+    if constexpr (R == kGemvRowsShaped) {
+      static_assert(M == 1 && XLDS, "flat and deep rows: one row of x in LDS");
+      if (nkw.w > kGemvFlat) {
+        if (nkw.y == 32 * 48)
+          gemv_rows_flat<48>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
+                             (half_t*)(gy_t)ptr.w, nkw.x, scale_shift, (gwave - nkw.z) * 4, lane);
+        else
+          gemv_rows_flat<32>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
+                             (half_t*)(gy_t)ptr.w, nkw.x, scale_shift, (gwave - nkw.z) * 2, lane);
+        return;
+      }
+      if (nkw.w == kGemvDeep) {
+        gemv_row_deep<kGemvDeepBlocks>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
+                         (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift, gwave - nkw.z, lane);
+        return;
+      }
+    }
     if (nkw.w == 3)
       gemv_rows<M, 3, UMAX, XLDS>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
                                   (const half_t*)(gh_t)ptr.z, (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift,
@@ -608,6 +814,10 @@ void* pick_r(int R, int U) {
   if (R == kGemvRowsMixed) {
     if constexpr (GROUPED && M <= 2) return pick_mixed<XLDS, M>(U);
     return nullptr;  // the plan never asks for it
+  }
+  if (R == kGemvRowsShaped) {  // the plan gives it unroll 1, M = 1 and x in LDS only
+    if constexpr (GROUPED && M == 1 && XLDS) return (void*)gemv_grouped_kernel<1, kGemvRowsShaped, 1, true>;
+    return nullptr;
   }
   return R == 1 ? pick_u<GROUPED, XLDS, M, 1>(U) : pick_u<GROUPED, XLDS, M, 2>(U);
 }
@@ -712,27 +922,62 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   // 6.9 -> 6.3 us on MI355X) wherever x fits the LDS budget.
   p.x_lds = x_lds_bytes(M, max_k) <= (size_t)kGemvMaxLdsX;
   for (int i = 0; i < count; ++i) p.rows[i] = p.rows_per_wave;
-  // A grouped launch whose two-row wavefronts outnumber the wave slots (8 per SIMD) runs
-  // its last wavefronts in a second round, a full memory round trip after the others.  The
-  // largest problems then take three rows per wavefront, just enough of them for the grid
-  // to fit (7 TinyLlama linears: 8,960 two-row wavefronts for 8,192 slots).
+  // Large grouped launches (two rows per wavefront) shape each problem's rows:
+  //   * M = 1, x in LDS: K = 1024 / 1536 problems take flat rows (full 1 KiB loads), and rows
+  //     longer than one 64-chunk block one row per wavefront with up to kGemvDeepBlocks blocks
+  //     per round trip, if the launch then still fits the wave slots (Qwen2.5's 7 linears at
+  //     M = 1: 6.85 -> 6.39 us on MI355X; TinyLlama's do not fit, and keep their plan).
+  //   * A launch whose wavefronts outnumber the wave slots (8 per SIMD) runs its last
+  //     wavefronts in a second round, a full memory round trip after the others.  The largest
+  //     two-row problems then take three rows per wavefront, just enough of them for the grid
+  //     to fit (7 TinyLlama linears: 8,960 two-row wavefronts for 8,192 slots).
   if (p.rows_per_wave == 2 && count > 1 && M <= 2) {
-    const long slots = 32L * cus;
     auto waves_of = [&](int i) {
-      long w = (N[i] + p.rows[i] - 1) / p.rows[i];
+      const int r = gemv_entry_rows(p.rows[i]);
+      long w = (N[i] + r - 1) / r;
       if (p.x_lds) w = (w + kGemvWavesPerBlock - 1) / kGemvWavesPerBlock * kGemvWavesPerBlock;
       return w;
     };
-    long total = 0;
-    for (int i = 0; i < count; ++i) total += waves_of(i);
-    while (total > slots) {
+    auto total_waves = [&]() {
+      long t = 0;
+      for (int i = 0; i < count; ++i) t += waves_of(i);
+      return t;
+    };
+    if (M == 1 && p.x_lds) {
+      for (int i = 0; i < count; ++i) {
+        const int f = gemv_flat_rows(K[i]);
+        if (f > 0) p.rows[i] = kGemvFlat + f;
+      }
+      bool deep = false;
+      for (int i = 0; i < count; ++i)
+        if (K[i] > 2048 && p.rows[i] == 2) {
+          p.rows[i] = kGemvDeep;
+          deep = true;
+        }
+      if (deep && total_waves() > 32L * cus) {
+        for (int i = 0; i < count; ++i)
+          if (p.rows[i] == kGemvDeep) p.rows[i] = 2;
+      }
+    }
+    const long slots = 32L * cus;
+    long total = total_waves();
+    bool three = false;
+    while (total > slots) {  // two-row problems (plain or flat) to three rows, largest first
       int best = -1;
       for (int i = 0; i < count; ++i)
-        if (p.rows[i] == 2 && (best < 0 || N[i] > N[best])) best = i;
+        if ((p.rows[i] == 2 || p.rows[i] == kGemvFlat + 2) && (best < 0 || N[i] > N[best])) best = i;
       if (best < 0) break;
       total -= waves_of(best);
       p.rows[best] = 3;
       total += waves_of(best);
+      three = true;
+    }
+    bool shaped = false;
+    for (int i = 0; i < count; ++i) shaped = shaped || p.rows[i] == kGemvDeep || p.rows[i] > kGemvFlat;
+    if (shaped) {
+      p.rows_per_wave = kGemvRowsShaped;
+      p.unroll = 1;
+    } else if (three) {
       p.rows_per_wave = kGemvRowsMixed;
     }
   }
@@ -769,7 +1014,7 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
       const GemvProblem& q = problems[order[i]];
       const int rows = plan.rows[order[i]];
       table.slot[i] = GemvSlot{q.x, q.packed, q.scales, q.y, q.N, q.K, waves, rows};
-      int w = ceil_div(q.N, rows);
+      int w = ceil_div(q.N, gemv_entry_rows(rows));
       if (plan.x_lds) w = ceil_div(w, kGemvWavesPerBlock) * kGemvWavesPerBlock;  // whole workgroups
       waves += w;
       bounds[i] = waves;

@@ -32,7 +32,7 @@ struct GemvSlot {
   int N;
   int K;
   int wave0;
-  int rows;  // rows per wavefront of this problem
+  int rows;  // rows per wavefront of this problem (2 or 3), kGemvFlat + F or kGemvDeep
 };
 
 // The grouped kernel's arguments: the lookup header as ten scalar arguments (preloaded into
@@ -52,11 +52,36 @@ constexpr int kGemvMaxLdsX = 20480;
 // each (GemvPlan::rows, GemvSlot::rows); also the grouped kernel's template rows for it.
 constexpr int kGemvRowsMixed = 3;
 
+// Flat rows (M = 1, grouped launches): a row of K = 32 C with C < 64 leaves E = 64 - C lanes of
+// every 64-chunk load idle.  When E divides C and C / E <= 3 (K = 1024: C = 32; K = 1536: C = 48)
+// one wavefront owns F = C / E + 1 rows in C / E full loads (gemv_rows_flat in kf_gemv.hip).  Such
+// a problem's GemvPlan::rows / GemvSlot::rows entry is kGemvFlat + F.  Returns F, or 0.
+constexpr int kGemvFlat = 16;
+inline int gemv_flat_rows(int K) {
+  if (K % 32 != 0 || K >= 2048) return 0;
+  const int c = K / 32, e = 64 - c;
+  return (e <= c && c % e == 0 && c / e <= 3) ? c / e + 1 : 0;
+}
+// Deep rows (M = 1, grouped launches with wavefront slots to spare): one long row per wavefront,
+// up to three 64-chunk blocks per memory round trip (gemv_row_deep in kf_gemv.hip).
+constexpr int kGemvDeep = 8;
+// GemvPlan::rows_per_wave of a grouped launch (M = 1, x in LDS) with flat or deep rows among its
+// problems.  Its kernel is an instantiation of its own, so launches without such rows keep the
+// mixed kernel's code and registers.  kGemvDeepBlocks: 64-chunk blocks per pass of a deep row,
+// as many as keep the kernel at 8 wavefronts per SIMD (kernelforge/build.py checks it; five
+// blocks cost one wavefront per SIMD and measured no faster on Qwen2.5's 7 linears).
+constexpr int kGemvRowsShaped = 4;
+constexpr int kGemvDeepBlocks = 4;
+// Rows one wavefront owns for a GemvPlan::rows / GemvSlot::rows entry.
+inline int gemv_entry_rows(int entry) {
+  return entry == kGemvDeep ? 1 : (entry > kGemvFlat ? entry - kGemvFlat : entry);
+}
+
 struct GemvPlan {
   int rows_per_wave;   // R: output rows one wavefront owns, or kGemvRowsMixed
   int unroll;          // U: 64-chunk blocks (64 lanes x 32 k) whose loads one pass keeps in flight
   bool x_lds;          // each workgroup copies x into LDS once (else every lane loads its x)
-  int rows[kMaxGemvGroup];  // rows per wavefront of each problem (in the caller's order)
+  int rows[kMaxGemvGroup];  // per problem (caller's order): rows per wavefront, kGemvFlat + F or kGemvDeep
 };
 GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count);
 hipError_t gemv_launch(const GemvPlan& p, const GemvProblem* problems, int count, int M, int group_size,

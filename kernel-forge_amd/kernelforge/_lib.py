@@ -24,6 +24,9 @@ KF_PROLOGUE_RMSNORM = 1
 KF_PROLOGUE_SWIGLU = 2
 KF_GEMV_FUSED_MAX_K = 10240
 KF_NOALLOC_SCRATCH_BYTES = 32 << 20
+KF_GEMV_KERNEL_ROWS1, KF_GEMV_KERNEL_ROWS2, KF_GEMV_KERNEL_MIXED, KF_GEMV_KERNEL_SHAPED = 1, 2, 3, 4
+KF_GEMV_DEEP = 8
+KF_GEMV_FLAT = 16
 
 GEMV_MAX_GROUP = 8
 
@@ -55,6 +58,7 @@ SIGNATURES = {
                                    _VP]),
     "kf_int4_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "kf_int4_gemm_plan": (_I, [_I, _I, _I, _I, _IP, _IP, _IP, _IP, _IP]),
+    "kf_int4_gemv_plan": (_I, [_I, _IP, _IP, _I, _I, _IP, _IP, _IP, _IP]),
     "kf_int4_gemm": (_I, [_VP, _VP, _VP, _VP, _VP, _SZ, _I, _I, _I, _I, _VP]),
     "kf_int4_gemm_noalloc": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "kf_int4_mfma16_sizes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
@@ -109,3 +113,18 @@ def check(status: int, what: str) -> None:
     if status in (KF_ERR_INVALID_ARG, KF_ERR_UNSUPPORTED):
         raise ValueError(msg)
     raise RuntimeError(msg)
+
+
+def gemv_plan(m: int, shapes: list[tuple[int, int]], cu_count: int = 0) -> dict:
+    """The GEMV launch plan (kf_int4_gemv_plan) for M and [(N, K), ...]: the kernel kind, each
+    problem's rows entry (1-3 rows per wavefront, KF_GEMV_FLAT + F or KF_GEMV_DEEP), the unroll and
+    whether x is staged in LDS.  Host-only when cu_count > 0 (no GPU needed)."""
+    lib = load()
+    count = len(shapes)
+    ns = (ctypes.c_int * count)(*[n for n, _ in shapes])
+    ks = (ctypes.c_int * count)(*[k for _, k in shapes])
+    kernel, unroll, x_lds = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rows = (ctypes.c_int * count)()
+    check(lib.kf_int4_gemv_plan(m, ns, ks, count, cu_count, ctypes.byref(kernel), rows, ctypes.byref(unroll),
+                                ctypes.byref(x_lds)), "int4_gemv_plan")
+    return {"kernel": kernel.value, "rows": list(rows), "unroll": unroll.value, "x_lds": bool(x_lds.value)}

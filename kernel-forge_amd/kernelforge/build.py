@@ -69,6 +69,14 @@ def _run(cmd: list[str], quiet_remarks: bool = False) -> str:
     return err
 
 
+# Kernels whose launch plan counts on an occupancy (kf_gemv.hip, gemv_plan: the grouped M = 1
+# launches, mixed and shaped, fit one resident round of 8 wavefronts per SIMD).
+MIN_OCCUPANCY = {
+    "gemv_grouped_kernelILi1ELi3ELi1ELb1E": 8,
+    "gemv_grouped_kernelILi1ELi4ELi1ELb1E": 8,
+}
+
+
 def _check_resources(remarks: str, src: str) -> None:
     """Every kernel must run from registers: no scratch (private segment) and no spills.  A
     kernel whose accumulators fall to scratch still gives right answers, 10-20x slower."""
@@ -81,6 +89,11 @@ def _check_resources(remarks: str, src: str) -> None:
         m = re.search(r"(ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill): (\d+)", line)
         if m and int(m.group(2)) > 0:
             bad.append(f"{name}: {m.group(1)} = {m.group(2)}")
+        m = re.search(r"Occupancy \[waves/SIMD\]: (\d+)", line)
+        if m and name:
+            for pattern, need in MIN_OCCUPANCY.items():
+                if pattern in name and int(m.group(1)) < need:
+                    bad.append(f"{name}: occupancy {m.group(1)} waves per SIMD, the launch plan assumes {need}")
     if bad:
         raise RuntimeError(f"{src}: kernels use scratch memory or spill registers:\n  " + "\n  ".join(bad))
 

@@ -7,6 +7,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from kernelforge import _lib
@@ -134,3 +135,99 @@ def test_qkv_rope_argument_errors_without_gpu():
     _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 2048, 128, None, eps, ctypes.byref(nul), None), "non-null")
     _err(lib.kf_int4_gemv_qkv_rope(p, p, p, p, 2560, 10240 + 128, 128, None, eps, ctypes.byref(rc), None),
          "K <= 10240")
+
+
+# ---------------------------------------------------------------------------
+# GEMV launch plan (host code: kf_int4_gemv_plan with an explicit CU count)
+# ---------------------------------------------------------------------------
+
+QWEN_SEVEN = [(1536, 1536), (256, 1536), (256, 1536), (1536, 1536), (8960, 1536), (8960, 1536), (1536, 8960)]
+TL_SEVEN = [(2048, 2048), (256, 2048), (256, 2048), (2048, 2048), (5632, 2048), (5632, 2048), (2048, 5632)]
+CUS = 256  # MI355X
+SLOTS = 32 * CUS  # 8 wavefronts per SIMD, 4 SIMDs per CU
+
+
+def _entry_rows(entry: int) -> int:
+    return 1 if entry == _lib.KF_GEMV_DEEP else (entry - _lib.KF_GEMV_FLAT if entry > _lib.KF_GEMV_FLAT else entry)
+
+
+def _waves(shapes, rows, x_lds) -> int:
+    total = 0
+    for (n, _), entry in zip(shapes, rows):
+        w = -(-n // _entry_rows(entry))
+        total += -(-w // 4) * 4 if x_lds else w
+    return total
+
+
+def test_gemv_plan_constants_match_header():
+    text = HEADER.read_text()
+    for name in ("KF_GEMV_KERNEL_ROWS1", "KF_GEMV_KERNEL_ROWS2", "KF_GEMV_KERNEL_MIXED", "KF_GEMV_KERNEL_SHAPED",
+                 "KF_GEMV_DEEP", "KF_GEMV_FLAT"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert m and int(m.group(1)) == getattr(_lib, name), name
+
+
+def test_gemv_plan_benchmarked_sets_without_gpu():
+    """The plans behind the benchmark's two 7-linear steps (M = 1, 256 CUs)."""
+    flat4 = _lib.KF_GEMV_FLAT + 4
+    qwen = _lib.gemv_plan(1, QWEN_SEVEN, CUS)
+    assert qwen["kernel"] == _lib.KF_GEMV_KERNEL_SHAPED and qwen["x_lds"] and qwen["unroll"] == 1
+    assert qwen["rows"] == [flat4] * 6 + [_lib.KF_GEMV_DEEP]  # K = 1536: 4 rows in 3 full loads; down: deep
+    assert _waves(QWEN_SEVEN, qwen["rows"], True) == 6912 <= SLOTS
+    tl = _lib.gemv_plan(1, TL_SEVEN, CUS)
+    # deep rows for down would need 9,984 wavefronts: the plan keeps two rows and gives gate three
+    assert tl["kernel"] == _lib.KF_GEMV_KERNEL_MIXED and tl["rows"] == [2, 2, 2, 2, 3, 2, 2]
+    assert _waves(TL_SEVEN, tl["rows"], True) == 8024 <= SLOTS
+
+
+def test_gemv_plan_rules_without_gpu():
+    flat2 = _lib.KF_GEMV_FLAT + 2
+    # many K = 1024 rows: flat two-row problems go to three rows, largest first, until the grid fits
+    heavy = [(9001, 1024), (8999, 1024), (4099, 1024), (257, 1024), (3, 1024), (1, 1024)]
+    p = _lib.gemv_plan(1, heavy, CUS)
+    assert p["kernel"] == _lib.KF_GEMV_KERNEL_SHAPED and p["rows"] == [3, 3, 3, flat2, flat2, flat2]
+    assert _waves(heavy, p["rows"], True) <= SLOTS
+    # flat and deep rows need M = 1 and x in LDS
+    for m in (2, 5, 8):
+        q = _lib.gemv_plan(m, QWEN_SEVEN, CUS)
+        assert all(r <= 3 for r in q["rows"]) and q["kernel"] != _lib.KF_GEMV_KERNEL_SHAPED
+    # single problems: one row per wavefront below 8 wavefronts per CU, else two
+    assert _lib.gemv_plan(1, [(2048, 2048)], CUS)["kernel"] == _lib.KF_GEMV_KERNEL_ROWS1
+    assert _lib.gemv_plan(1, [(5632, 2048)], CUS)["kernel"] == _lib.KF_GEMV_KERNEL_ROWS2
+    # K = 1536 / 1024 rows in a small launch keep one row per wavefront (no flat rows)
+    small = _lib.gemv_plan(1, [(256, 1536), (256, 1024)], CUS)
+    assert small["kernel"] == _lib.KF_GEMV_KERNEL_ROWS1 and small["rows"] == [1, 1]
+
+
+def test_gemv_plan_fits_one_round_without_gpu():
+    """Random grouped launches at M = 1 and 2: whenever the plan leaves a two-row problem (plain
+    or flat) it has found a grid that fits the 8,192 wave slots; deep rows appear only in grids
+    that fit; flat rows only for K = 1024 / 1536."""
+    rng = np.random.default_rng(7)
+    for _ in range(300):
+        count = int(rng.integers(2, 9))
+        shapes = [(int(rng.integers(1, 12000)), int(rng.choice([512, 1024, 1536, 2048, 3072, 5632, 8960])))
+                  for _ in range(count)]
+        for m in (1, 2):
+            p = _lib.gemv_plan(m, shapes, CUS)
+            rows = p["rows"]
+            if p["kernel"] in (_lib.KF_GEMV_KERNEL_MIXED, _lib.KF_GEMV_KERNEL_SHAPED):
+                waves = _waves(shapes, rows, p["x_lds"])
+                if any(r in (2, _lib.KF_GEMV_FLAT + 2) for r in rows) or _lib.KF_GEMV_DEEP in rows:
+                    assert waves <= SLOTS, (m, shapes, p)
+            for (n, k), r in zip(shapes, rows):
+                if r > _lib.KF_GEMV_FLAT:
+                    assert m == 1 and k in (1024, 1536) and r == _lib.KF_GEMV_FLAT + (4 if k == 1536 else 2)
+                if r == _lib.KF_GEMV_DEEP:
+                    assert m == 1 and k > 2048
+
+
+def test_gemv_plan_argument_errors_without_gpu():
+    lib = _lib.load()
+    one = (ctypes.c_int * 1)(64)
+    k = (ctypes.c_int * 1)(256)
+    _err(lib.kf_int4_gemv_plan(1, None, k, 1, CUS, None, None, None, None), "non-null")
+    _err(lib.kf_int4_gemv_plan(1, one, k, 9, CUS, None, None, None, None), "count")
+    _err(lib.kf_int4_gemv_plan(9, one, k, 1, CUS, None, None, None, None), r"M in \[1, 8\]")
+    bad = (ctypes.c_int * 1)(200)
+    _err(lib.kf_int4_gemv_plan(1, one, bad, 1, CUS, None, None, None, None), "multiple of 64")

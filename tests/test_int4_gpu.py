@@ -159,8 +159,8 @@ QWEN_SEVEN = [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536,
 @pytest.mark.parametrize("group", [64, 128])
 def test_grouped_qwen_seven_as_benchmarked(error_log, group):
     """BASELINE config 3 exactly as bench.py times it: the 7 Qwen2.5-1.5B linears in one grouped
-    launch at M = 1 (mixed two- and three-row wavefronts), each output bit-identical to its own
-    GEMV launch and within tolerance of the oracle."""
+    launch at M = 1 (flat rows for the six K = 1536 linears, deep rows for down), each output
+    bit-identical to its own GEMV launch and within tolerance of the oracle."""
     xs, ps, ss, refs = [], [], [], []
     for i, (_, n, k) in enumerate(QWEN_SEVEN):
         packed, scales, dp, ds = _weights(n, k, group)
@@ -428,35 +428,64 @@ def test_output_guard_bands(kind, m, n, k):
     assert o.max_rel_err(y, o.linear_ref_fp32(_x(m, k, 5), packed, scales, g)) <= REL_TOL
 
 
-@pytest.mark.parametrize("m", [1, 2])
-def test_grouped_guard_bands_three_row_waves(m):
-    """A grouped launch too large for one resident round at two rows per wavefront (> 8 per SIMD),
-    so its largest problems take three rows: ragged N (not a multiple of 3), every output inside
-    its guard bands, bit-identical to its own single launch, within tolerance of the oracle."""
-    g, k = 128, 1024
-    ns = [9001, 8999, 4099, 257, 3, 1]
+def _grouped_guarded(m: int, shapes, g: int, seed: int):
+    """One kf_int4_gemv_grouped launch with every y inside guard bands; checks that nothing is
+    written outside y, every element is written, each y equals its own single GEMV launch bit
+    for bit and the oracle within tolerance."""
     guard = 2048
     sentinel = torch.tensor(-12345.0, dtype=torch.float16)
     lib = _lib.load()
     stream = torch.cuda.current_stream().cuda_stream
     cases, bufs = [], []
-    probs = (_lib.GemvProblem * len(ns))()
-    for i, n in enumerate(ns):
+    probs = (_lib.GemvProblem * len(shapes))()
+    for i, (n, k) in enumerate(shapes):
         packed, scales, dp, ds = _weights(n, k, g)
-        xh = _x(m, k, 300 + i)
+        xh = _x(m, k, seed + i)
         x = torch.from_numpy(xh).to(DEV)
         buf = torch.full((guard + m * n + guard,), float(sentinel), dtype=torch.float16, device=DEV)
         probs[i] = _lib.GemvProblem(x.data_ptr(), dp.data_ptr(), ds.data_ptr(), buf.data_ptr() + 2 * guard, n, k)
-        cases.append((n, xh, x, packed, scales, dp, ds))
+        cases.append((n, k, xh, x, packed, scales, dp, ds))
         bufs.append(buf)
-    _lib.check(lib.kf_int4_gemv_grouped(probs, len(ns), m, g, stream), "int4_gemv_grouped")
-    for (n, xh, x, packed, scales, dp, ds), buf in zip(cases, bufs):
+    _lib.check(lib.kf_int4_gemv_grouped(probs, len(shapes), m, g, stream), "int4_gemv_grouped")
+    for (n, k, xh, x, packed, scales, dp, ds), buf in zip(cases, bufs):
         host = buf.cpu()
-        assert (host[:guard] == sentinel).all() and (host[guard + m * n:] == sentinel).all(), f"N={n}: write outside y"
+        what = f"N={n} K={k}"
+        assert (host[:guard] == sentinel).all() and (host[guard + m * n:] == sentinel).all(), f"{what}: write outside y"
         y = host[guard:guard + m * n].reshape(m, n)
-        assert not (y == sentinel).any(), f"N={n}: unwritten output element"
-        assert torch.equal(y.to(DEV), ops.int4_gemv(x, dp, ds, g)), f"N={n}: grouped differs from single"
-        assert o.max_rel_err(y.float().numpy(), o.linear_ref_fp32(xh, packed, scales, g)) <= REL_TOL
+        assert not (y == sentinel).any(), f"{what}: unwritten output element"
+        assert torch.equal(y.to(DEV), ops.int4_gemv(x, dp, ds, g)), f"{what}: grouped differs from single"
+        assert o.max_rel_err(y.float().numpy(), o.linear_ref_fp32(xh, packed, scales, g)) <= REL_TOL, what
+
+
+@pytest.mark.parametrize("m,k", [(1, 1024), (2, 1024), (1, 2048), (2, 2048)])
+def test_grouped_guard_bands_three_row_waves(m, k):
+    """A grouped launch too large for one resident round at two rows per wavefront (> 8 per SIMD),
+    so its largest problems take three rows: ragged N (not a multiple of 3), every output inside
+    its guard bands, bit-identical to its own single launch, within tolerance of the oracle.  At
+    M = 1, K = 1024 the small problems keep flat rows (two rows in one full load)."""
+    ns = [9001, 8999, 4099, 257, 3, 1]
+    shapes = [(n, k) for n in ns]
+    plan = _lib.gemv_plan(m, shapes)
+    assert 3 in plan["rows"], plan
+    if m == 1 and k == 1024:
+        assert plan["rows"][3:] == [_lib.KF_GEMV_FLAT + 2] * 3, plan
+    _grouped_guarded(m, shapes, 128, 300)
+
+
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_flat_and_deep_rows(group):
+    """The shaped grouped launch (M = 1): flat rows for K = 1536 (four rows in three full loads) and
+    K = 1024 (two rows in one), with N leaving the last wavefront part empty, and deep rows for
+    K = 8960 (a four-block pass, then 24 chunks), 6144 (one three-block pass) and 2304 (one
+    two-block pass of 72 chunks), beside a plain two-row problem: outputs inside their guard
+    bands, bit-identical to single launches, within tolerance of the oracle."""
+    shapes = [(1534, 1536), (1023, 1024), (3001, 1536), (701, 8960), (515, 2304), (257, 2048), (6, 1536),
+              (130, 6144)]
+    plan = _lib.gemv_plan(1, shapes)
+    flat4, flat2, deep = _lib.KF_GEMV_FLAT + 4, _lib.KF_GEMV_FLAT + 2, _lib.KF_GEMV_DEEP
+    assert plan["kernel"] == _lib.KF_GEMV_KERNEL_SHAPED, plan
+    assert plan["rows"] == [flat4, flat2, flat4, deep, deep, 2, flat4, deep], plan
+    _grouped_guarded(1, shapes, group, 700)
 
 
 # ---------------------------------------------------------------------------
