@@ -6,11 +6,13 @@
 // fixed split order (deterministic), the behaviour of the reference's splitk_reduce
 // (dequant_gemm_tc_kernel.cuh:156-162).
 //
-// Two kernel families share one tile table (kTiles below; gemm_plan picks an entry and a
+// Three kernel families share one tile table (kTiles below; gemm_plan picks an entry and a
 // split-K factor with a fitted cost model):
 //   * gemm_kernel<TileCfg>: register-staged LDS tiles, 64 x 128 down to 16 x 64;
 //   * gemm_dma_kernel<KW>: 128 x 128 tiles fed by LDS-DMA, 2 (4 wavefronts) or 4 (8 wavefronts)
-//     k-groups; see the comment above the kernel.
+//     k-groups; see the comment above the kernel;
+//   * gemm_wide_kernel: 192 x 256 tiles fed by LDS-DMA, 8 wavefronts, one workgroup per CU, for
+//     grids of about one tile per CU (half the L2 -> LDS bytes per output of the 128 x 128 tiles).
 //
 // Design of gemm_kernel (gfx950: 4 SIMDs per CU, ~2 VALU ops hide under one 16x16x32 MFMA,
 // LDS reads ~150-200 B/clk per CU):
@@ -645,6 +647,209 @@ void gemm_dma_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ 
   }
 }
 
+// Wide DMA-fed tile: 192 x 256 per workgroup, 8 wavefronts as 2 x 4 wave tiles of 96 x 64, every
+// wavefront over the whole 64-k stage (no k split, no partial-tile reduction), one workgroup per
+// CU (99 KiB of stages and scale ring).  Per 64-k stage a CU moves 32 KiB from L2 into LDS for
+// 192 x 256 outputs, against 40 KiB for the two 128 x 128 tiles of gemm_dma_kernel<2> (half the
+// outputs): x, fp16 and the larger operand, is re-read from L2 once per 256 columns instead of
+// once per 128.  Stage pipeline, swizzles, scale ring and counted waits are those of
+// gemm_dma_kernel<2>.  MI355X, M = 2048, N = 5632, K = 2048 (242 tiles, one per CU): 52 us = 906
+// TFLOPS against 56 us for the 128 x 128 tiles.  A tile alone on its CU takes 44 us (K = 2048), so
+// the tile pays only where its count fills whole rounds of 256; gemm_plan weighs that.
+struct WideCfg {
+  static constexpr int BM = 192, BN = 256, BK = 64, NS = 3, WM = 2, WN = 4, WAVES = WM * WN, THREADS = 64 * WAVES;
+  static constexpr int TM = 6, TN = 4;               // 16 x 16 blocks per wavefront
+  static constexpr int A_ROW = BK * 2;               // 128 bytes of x per row and stage
+  static constexpr int A_CH = BK / 8;                // 8 chunks of 16 bytes
+  static constexpr int A_BYTES = BM * A_ROW;         // 24 KiB
+  static constexpr int B_OFF = A_BYTES;
+  static constexpr int B_ROW = BK / 2;               // 32 bytes of packed weights per row and stage
+  static constexpr int B_CH = BK / 32;               // 2 chunks
+  static constexpr int B_BYTES = BN * B_ROW;         // 8 KiB
+  static constexpr int STAGE = B_OFF + B_BYTES;
+  static constexpr int S_SLAB = BN * 4;              // [BN] 4-byte slots
+  static constexpr int S_RING = NS * STAGE;
+  static constexpr int RING_END = S_RING + NS * S_SLAB;
+  static constexpr int OUT_ROW = BN * 2 + 16;
+  static constexpr int SMEM = RING_END > BM * OUT_ROW ? RING_END : BM * OUT_ROW;
+  static constexpr int A_DMA = A_BYTES / 1024 / WAVES;  // 3 x instructions per wavefront and stage
+  static constexpr int kDmaPerStage = A_DMA + 1;        // + 1 packed
+  static_assert(A_DMA * 1024 * WAVES == A_BYTES && B_BYTES == 1024 * WAVES, "DMA split");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+};
+
+__global__ __launch_bounds__(WideCfg::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_wide_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
+                      const half_t* __restrict__ scales, half_t* __restrict__ y, float* __restrict__ ws, int M, int N,
+                      int K, int log2_group, int stages_per_split, int splits, int tiles_m, int tiles_n,
+                      int group_m) {
+  using C = WideCfg;
+  constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NS = C::NS, THREADS = C::THREADS, TM = C::TM, TN = C::TN;
+  constexpr int A_ROW = C::A_ROW, B_ROW = C::B_ROW, B_OFF = C::B_OFF, STAGE = C::STAGE, OUT_ROW = C::OUT_ROW;
+  constexpr int kDmaPerStage = C::kDmaPerStage, A_DMA = C::A_DMA;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[C::SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 3;
+  const int wm = wave >> 2;
+  const int g = lane >> 4;
+  const int l16 = lane & 15;
+
+  int split, t;
+  if (!gemm_job(tiles_m * tiles_n, splits, split, t)) return;
+  const int band = group_m * tiles_n;
+  const int bi = t / band;
+  const int tb = t - bi * band;
+  const int gm = min(group_m, tiles_m - bi * group_m);
+  const int m0 = (bi * group_m + tb % gm) * BM;
+  const int n0 = (tb / gm) * BN;
+
+  const int nst = K / BK;
+  const int st_begin = split * stages_per_split;
+  const int last = min(nst, st_begin + stages_per_split) - 1;
+  const int ns = last + 1 - st_begin;
+
+  // XOR swizzles: x chunk c of row r at slot c ^ a_swz(r); packed chunk h of row r at h ^ b_swz(r).
+  auto a_swz = [](int row) { return (row >> 1) & (C::A_CH - 1); };
+  auto b_swz = [](int row) { return (row >> 3) & (C::B_CH - 1); };
+
+  // DMA sources at k = 0.  x: A_DMA instructions of 1 KiB (8 rows) per wavefront; packed: one
+  // of 1 KiB (32 rows).
+  const half_t* a_src[A_DMA];
+#pragma unroll
+  for (int q = 0; q < A_DMA; ++q) {
+    const int row = 8 * (A_DMA * wave + q) + (lane >> 3);
+    a_src[q] = x + (size_t)min(m0 + row, M - 1) * K + 8 * ((lane & 7) ^ a_swz(row));
+  }
+  const int brow = 32 * wave + (lane >> 1);
+  const uint32_t* b_src = packed + (size_t)min(n0 + brow, N - 1) * (K >> 3) + 4 * ((lane & 1) ^ b_swz(brow));
+  const int groups = K >> log2_group;
+  const half_t* s_src = scales + (size_t)min(n0 + 64 * wn + lane, N - 1) * groups;
+  const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
+
+  const int log2_spg = log2_group - 6;  // log2(stages per group)
+  auto starts_group = [&](int i) {
+    const int st = st_begin + i;
+    return i == 0 || (st <= last && (st & ((1 << log2_spg) - 1)) == 0);
+  };
+  auto group_of = [&](int i) { return ((st_begin + i) >> log2_spg) - (st_begin >> log2_spg); };
+  auto issue = [&](int i, int buf) {
+    const int st = min(st_begin + i, last);
+    const int k0 = st * BK;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)(buf * STAGE));
+#pragma unroll
+    for (int q = 0; q < A_DMA; ++q) dma_16B(base + 1024 * (A_DMA * wave + q), a_src[q] + k0);
+    dma_16B(base + B_OFF + 1024 * wave, b_src + (k0 >> 3));
+    const bool sc = wm == 0 && starts_group(i);
+    if (sc) {
+      const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+          smem_base + (uint32_t)(C::S_RING + (group_of(i) % NS) * C::S_SLAB + 256 * wn));
+      dma_u16(sbase, s_src + (k0 >> log2_group));
+    }
+    return sc;
+  };
+  auto wait_older = [&](bool newer_has_scales) {
+    if (newer_has_scales)
+      wait_vmcnt<kDmaPerStage + 1>();
+    else
+      wait_vmcnt<kDmaPerStage>();
+  };
+
+  float4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Lane offsets: x row 96 wm + l16 (+16 per block), chunk 4 kk + g; packed row 64 wn + 16 j + l16,
+  // chunk kk, dword g; scales column 64 wn + 16 j + l16.
+  const int a_row0 = 96 * wm + l16;
+  const int a_off0 = a_row0 * A_ROW + 16 * ((0 + g) ^ a_swz(a_row0));
+  const int a_off1 = a_row0 * A_ROW + 16 * ((4 + g) ^ a_swz(a_row0));
+  const int b_row0 = 64 * wn + l16;
+  const int b_off0 = B_OFF + b_row0 * B_ROW + 16 * (0 ^ b_swz(b_row0)) + 4 * g;
+  const int b_off1 = B_OFF + b_row0 * B_ROW + 16 * (1 ^ b_swz(b_row0)) + 4 * g;
+  const int s_off = 4 * (64 * wn + l16);
+
+  const UnpackConsts uc = unpack_consts();
+  half8_t a[2][TM];
+  uint32_t w[2][TN];
+  half2_t s2[TN];
+  auto read_frags = [&](int i, int buf) {
+    const unsigned char* st = smem + buf * STAGE;
+    const unsigned char* slab = smem + C::S_RING + (group_of(i) % NS) * C::S_SLAB;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      w[0][j] = *reinterpret_cast<const uint32_t*>(st + b_off0 + 16 * B_ROW * j);
+      w[1][j] = *reinterpret_cast<const uint32_t*>(st + b_off1 + 16 * B_ROW * j);
+      const half_t sc = *reinterpret_cast<const half_t*>(slab + s_off + 64 * j);
+      s2[j] = half2_t{sc, sc};
+    }
+#pragma unroll
+    for (int q = 0; q < TM; ++q) {
+      a[0][q] = *reinterpret_cast<const half8_t*>(st + a_off0 + 16 * A_ROW * q);
+      a[1][q] = *reinterpret_cast<const half8_t*>(st + a_off1 + 16 * A_ROW * q);
+    }
+  };
+
+  issue(0, 0);
+  wait_older(issue(1, 1));
+  __syncthreads();
+  // Stage pipeline of gemm_dma_kernel: stage i's fragments (both 32-k steps) are read at
+  // iteration i, before the barrier after which stage i + 2's DMA may overwrite stage i - 1's
+  // buffer; the scheduling barrier keeps the next stage's reads out of this stage's MFMAs.
+  auto step = [&](auto buf_c, int s) {
+    constexpr int CUR = decltype(buf_c)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(s, CUR);
+    wait_older(issue(s + 2, (CUR + 2) % NS));
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const half8_t b = dequant8(w[kk][j], s2[j], uc);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kk][i], b, acc[i][j], 0, 0, 0);
+      }
+  };
+  // Whole rounds of NS stages, then the remaining one or two: an exit in the middle of the
+  // unrolled round made the compiler copy the accumulators between its copies of the round and
+  // spill (256 VGPRs + 111 spilled against 236 without).
+  static_assert(NS == 3, "the unrolled loop below assumes three stages");
+  int s = 0;
+  for (; s + NS <= ns; s += NS) {
+    step(std::integral_constant<int, 0>(), s);
+    step(std::integral_constant<int, 1>(), s + 1);
+    step(std::integral_constant<int, 2>(), s + 2);
+  }
+  if (s < ns) step(std::integral_constant<int, 0>(), s);
+  if (s + 1 < ns) step(std::integral_constant<int, 1>(), s + 1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // fp16 tile through LDS, then 16-byte row-major stores by all wavefronts (no split-K: ws unused).
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<half_t*>(smem + (96 * wm + 16 * i + 4 * g + r) * OUT_ROW + 2 * (64 * wn + 16 * j + l16)) =
+            (half_t)acc[i][j][r];
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < BM * BN / 8 / THREADS; ++q) {
+    const int c = tid + THREADS * q;
+    const int row = c >> 5, chunk = c & 31;
+    const int gr = m0 + row, gc = n0 + 8 * chunk;
+    if (gr < M && gc < N)
+      *reinterpret_cast<u32x4*>(y + (size_t)gr * N + gc) = *reinterpret_cast<const u32x4*>(smem + row * OUT_ROW + 16 * chunk);
+  }
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, half_t* __restrict__ y,
                                                       size_t mn, int splits) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < mn; i += (size_t)gridDim.x * 256) {
@@ -672,23 +877,27 @@ TileEntry entry(int blocks_per_cu, double us_per_gmac, double us_fixed) {
   return TileEntry{C::BM, C::BN, C::SK, C::THREADS, blocks_per_cu, us_per_gmac, us_fixed, gemm_kernel<C>};
 }
 
-// Tile table: index = GemmPlan::tile.  Cost terms: least-squares fit (log-time) of the model
-// in gemm_plan to graph-replayed timings of every tile and split count over the TinyLlama and
-// Qwen2.5 layer shapes, M = 16 .. 4096, on MI355X (4,172 points, rms error 7.0%).
+// Tile table: index = GemmPlan::tile.  Cost terms: weighted least-squares fit (relative error)
+// of the model in gemm_plan to graph-replayed timings of every tile and split count 1..12 over
+// the TinyLlama and Qwen2.5 layer shapes, M = 48 .. 4096, weights rotated through more than
+// twice the MALL, on MI355X (4,172 points, rms error 7.7%).  Over those shapes the plan's
+// choices take 1.0074x the time of the best measured (tile, split) per shape (1.0122x without
+// the 192 x 256 tile).
 const TileEntry kTiles[] = {
     entry<TileCfg<64, 128, 1, 4, 1>>(0, 0.0, 0.0),         // 0: 64 x 128, 4 waves; 64-k stages (any K)
-    entry<TileCfg<64, 128, 1, 4, 2>>(1, 630.70, 2.863),    // 1: 64 x 128, 8 waves (2 k-groups)
-    TileEntry{128, 128, DmaCfg<2>::BK, DmaCfg<2>::THREADS, 2, 543.09, 5.333, gemm_dma_kernel<2>},  // 2: DMA 128 x 128
-    entry<TileCfg<32, 128, 1, 4, 2>>(1, 915.33, 1.981),    // 3: 32 x 128, 8 waves (2 k-groups)
-    entry<TileCfg<32, 64, 1, 2, 4>>(1, 1036.37, 2.430),    // 4: 32 x 64, 8 waves (4 k-groups, 256-k stages)
-    entry<TileCfg<16, 64, 1, 2, 4>>(1, 1760.44, 1.894),    // 5: 16 x 64, 8 waves (4 k-groups, 256-k stages)
-    TileEntry{128, 128, DmaCfg<4>::BK, DmaCfg<4>::THREADS, 1, 375.53, 6.692, gemm_dma_kernel<4>},  // 6: DMA, 8 waves
+    entry<TileCfg<64, 128, 1, 4, 2>>(1, 702.21, 2.867),    // 1: 64 x 128, 8 waves (2 k-groups)
+    TileEntry{128, 128, DmaCfg<2>::BK, DmaCfg<2>::THREADS, 2, 557.73, 5.918, gemm_dma_kernel<2>},  // 2: DMA 128 x 128
+    entry<TileCfg<32, 128, 1, 4, 2>>(1, 999.91, 1.977),    // 3: 32 x 128, 8 waves (2 k-groups)
+    entry<TileCfg<32, 64, 1, 2, 4>>(1, 1081.97, 2.779),    // 4: 32 x 64, 8 waves (4 k-groups, 256-k stages)
+    entry<TileCfg<16, 64, 1, 2, 4>>(1, 1831.66, 2.117),    // 5: 16 x 64, 8 waves (4 k-groups, 256-k stages)
+    TileEntry{128, 128, DmaCfg<4>::BK, DmaCfg<4>::THREADS, 1, 388.59, 7.265, gemm_dma_kernel<4>},  // 6: DMA, 8 waves
+    TileEntry{192, 256, WideCfg::BK, WideCfg::THREADS, 1, 387.22, 4.351, gemm_wide_kernel},  // 7: DMA 192 x 256
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-constexpr int kTile64 = 0, kDmaTile = 2;
+constexpr int kTile64 = 0, kDmaTile = 2, kWideTile = 7;
 // Split-K costs one more launch plus the fp32 partials: kSplitUs + kSplitUsPerElem * splits * M * N
 // (same fit), and is taken only when the model predicts it at least 10% faster.
-constexpr double kSplitUs = 2.924, kSplitUsPerElem = 1.5826e-6, kSplitMargin = 0.9;
+constexpr double kSplitUs = 4.352, kSplitUsPerElem = 1.3750e-6, kSplitMargin = 0.9;
 constexpr int kMaxSplits = 12;  // the largest split count the fit was measured on
 
 GemmPlan plan_for(int K, int tile, int splits) {
@@ -755,7 +964,8 @@ GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
     if (e.blocks_per_cu == 0 || K % e.sk != 0) continue;
     const int nst = K / e.sk;
     const long tiles = (long)ceil_div(M, e.bm) * ceil_div(N, e.bn);
-    const int max_splits = std::min(kMaxSplits, std::max(1, nst / 4));  // >= 4 stages per split
+    // >= 4 stages per split; the 192 x 256 tile never splits (its kernel writes no partials)
+    const int max_splits = tile == kWideTile ? 1 : std::min(kMaxSplits, std::max(1, nst / 4));
     int prev = 0;
     for (int s = 1; s <= max_splits; ++s) {
       const int splits = ceil_div(nst, ceil_div(nst, s));

@@ -239,7 +239,7 @@ def test_gemm_n_multiple_of_64_not_128(error_log, n):
 # K % 128 != 0.  (M, N, K) -> kernel/splits as the dispatcher picks them on 256 CUs.
 EDGE_CASES = [(513, 2112, 384), (1000, 320, 4224), (1000, 2112, 384), (1500, 640, 8960), (33, 64, 1152),
               (33, 320, 4224), (300, 960, 2048), (33, 192, 2304), (33, 640, 8960), (47, 704, 5120),
-              (130, 1600, 640), (65, 192, 4160), (900, 1472, 6272), (600, 1216, 7424)]
+              (130, 1600, 640), (65, 192, 4160), (900, 1472, 6272), (600, 1216, 7424), (1300, 6080, 640)]
 
 
 @pytest.mark.parametrize("m,n,k", EDGE_CASES)
