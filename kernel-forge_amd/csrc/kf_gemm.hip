@@ -235,7 +235,7 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
     for (int j = 0; j < C::TN; ++j) {
       const half8_t b = dequant8(w[j], sc[j]);
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[i][j], 0, 0, 0);
+      for (int i = 0; i < C::TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, a[i], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -317,25 +317,27 @@ void gemm_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ pack
               &red[((q - 1) * C::WGM * C::WGN + wmn) * WAVE_FLOATS + (i * C::TN + j) * 256 + 4 * lane]);
   }
 
-  // 16x16 MFMA result layout: lane l, element r holds row 4*(l/16)+r, column l%16.
+  // The MFMAs take the weights as their first operand, so each 16 x 16 block comes out transposed:
+  // lane l, element r holds y row l%16, column 4*(l/16)+r.  A lane stores its four consecutive
+  // columns at once (8 bytes of y or 16 of fp32 partials); N % 64 == 0 keeps them inside the row.
   float* part = ws ? ws + (size_t)split * M * N : nullptr;
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int i = 0; i < C::TM; ++i) {
+    const int row = m0 + (wm * C::TM + i) * 16 + l16;
+    if (row >= M) continue;
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
-      const int col = n0 + (wn * C::TN + j) * 16 + l16;
+      const int col = n0 + (wn * C::TN + j) * 16 + 4 * g;
       if (col >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + (wm * C::TM + i) * 16 + 4 * g + r;
-        if (row < M) {
-          if (part)
-            part[(size_t)row * N + col] = acc[i][j][r];
-          else
-            y[(size_t)row * N + col] = (half_t)acc[i][j][r];
-        }
+      if (part) {
+        *reinterpret_cast<float4_t*>(part + (size_t)row * N + col) = acc[i][j];
+      } else {
+        const half2_t lo = {(half_t)acc[i][j][0], (half_t)acc[i][j][1]};
+        const half2_t hi = {(half_t)acc[i][j][2], (half_t)acc[i][j][3]};
+        *reinterpret_cast<u32x2*>(y + (size_t)row * N + col) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
       }
     }
+  }
 }
 
 // ---- DMA-fed kernel: 128 x 128 tile, KW k-groups (KW = 2: 4 wavefronts, 64-k stages;
