@@ -28,11 +28,17 @@ __device__ __forceinline__ To bit_cast(const From& v) {
   return __builtin_bit_cast(To, v);
 }
 
-// q pair (k 2i, k 2i+1) of a packed word as exact fp16 integers.
+// q pair (k 2i, k 2i+1) of a packed word as exact fp16 integers.  Nibble pair I sits at bits
+// 4I (low half) and 16 + 4I (high half).  A nibble u at mantissa bits 0-3 under exponent 2^10
+// (0x6400) reads 1024 + u; at mantissa bits 4-7 under exponent 2^6 (0x5400) it reads
+// 64 + 16u / 16 = 64 + u.  So pairs 0 and 1 come from the word itself and pairs 2 and 3 from the
+// word shifted by 8, one shift per word instead of three; q = u - 8 = v - 1032 or v - 72, exact.
 template <int I>
 __device__ __forceinline__ half2_t nibble_pair(uint32_t w) {
-  const uint32_t v = ((w >> (4 * I)) & 0x000F000Fu) | 0x64006400u;
-  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  const uint32_t src = I >= 2 ? (w >> 8) : w;
+  const uint32_t v = (I & 1) ? ((src & 0x00F000F0u) | 0x54005400u) : ((src & 0x000F000Fu) | 0x64006400u);
+  const half_t b = (I & 1) ? (half_t)72.0f : (half_t)1032.0f;
+  const half2_t bias = {b, b};
   return bit_cast<half2_t>(v) - bias;
 }
 
@@ -56,26 +62,38 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, half2_t s2) {
   return out;
 }
 
-// The same unpack with its two constants held in registers.  gfx9 VOP3 encodings take no
-// literal operand and at most one SGPR, so without this the compiler splits every
-// v_and_or_b32 into v_and_b32 + v_or_b32 (19 instead of 15 VALU ops per word).  The
-// constants come from opaque moves, made once per kernel, that the compiler cannot fold.
+// The same unpack with its masks and magic numbers held in registers.  gfx9 VOP3 encodings take
+// no literal operand and at most one SGPR, so without this the compiler splits every
+// v_and_or_b32 into v_and_b32 + v_or_b32.  With them a word costs 13 VALU ops: one shift, four
+// v_and_or_b32, four packed subtracts and four packed scale multiplies (15 when every pair
+// needed its own shift).  The constants come from opaque moves, made once per kernel, that the
+// compiler cannot fold.
 struct UnpackConsts {
-  uint32_t mask;   // 0x000F000F, in an SGPR
-  uint32_t magic;  // 0x64006400, in a VGPR
+  uint32_t mask;      // 0x000F000F, in an SGPR
+  uint32_t mask_hi;   // 0x00F000F0, in an SGPR
+  uint32_t magic;     // 0x64006400, in a VGPR
+  uint32_t magic_hi;  // 0x54005400, in a VGPR
 };
 __device__ __forceinline__ UnpackConsts unpack_consts() {
   UnpackConsts c;
   asm("s_mov_b32 %0, 0x000f000f" : "=s"(c.mask));
+  asm("s_mov_b32 %0, 0x00f000f0" : "=s"(c.mask_hi));
   asm("v_mov_b32 %0, 0x64006400" : "=v"(c.magic));
+  asm("v_mov_b32 %0, 0x54005400" : "=v"(c.magic_hi));
   return c;
 }
 
+// nibble_pair<I>(w) with one v_and_or_b32 per pair (see above for the two encodings).
 template <int I>
 __device__ __forceinline__ half2_t nibble_pair(uint32_t w, const UnpackConsts& c) {
   uint32_t v;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(v) : "v"(I ? (w >> (4 * I)) : w), "s"(c.mask), "v"(c.magic));
-  const half2_t bias = {(half_t)1032.0f, (half_t)1032.0f};
+  const uint32_t src = I >= 2 ? (w >> 8) : w;
+  if constexpr (I & 1)
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(v) : "v"(src), "s"(c.mask_hi), "v"(c.magic_hi));
+  else
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(v) : "v"(src), "s"(c.mask), "v"(c.magic));
+  const half_t b = (I & 1) ? (half_t)72.0f : (half_t)1032.0f;
+  const half2_t bias = {b, b};
   return bit_cast<half2_t>(v) - bias;
 }
 
