@@ -22,12 +22,15 @@ timed and reported beside it:
 Protocol
 * Infinity-Cache-cold: R copies of the 7-layer weight set (R * 22.8 MB >= 2x
   the 256 MB MALL) are rotated, step i using copy i % R.
-* Steps are captured in HIP graphs (R steps per graph; host launch cost is
-  excluded, as in the reference's CUDA-graph decode).  Every graph is captured
-  before timing; then W warm-up steps and exactly K timed steps, bracketed by
+* W warm-up steps, then exactly K timed steps, bracketed by
   torch.cuda.synchronize() and timed by a HIP event pair on the launching
-  stream behind a short GPU spin (the reference's launch guard).  The host wall
-  clock over the same K steps is reported beside it.
+  stream behind a GPU spin (the reference's launch guard), so host launch cost
+  is excluded.  K <= 512: the K steps are eager launches of the op's C-ABI call
+  with each weight copy's problem table built once, queued behind a spin longer
+  than their enqueue (a HIP graph launch has ~6 us of fixed cost on ROCm, 5% of
+  the step at K = 20); larger K: replays of HIP graphs (R steps per graph, as in
+  the reference's CUDA-graph decode), all captured before timing.  The graph
+  timing of the same K and the host wall clock are reported beside it.
 * roofline: the dominant kernel is the grouped GEMV (the whole step, one launch
   per step), so its average duration per launch is the timed region's event
   time / K; achieved = 22,779,904 B / that duration.
@@ -357,6 +360,78 @@ class GraphSteps:
         return self.timed(count)[0]
 
 
+BOUND_MAX_STEPS = 512  # longest timed region run as eager launches behind one spin (BoundSteps)
+
+
+class BoundSteps:
+    """The headline step as eager launches of kf_int4_gemv_grouped, the C-ABI call
+    ops.int4_linear_grouped makes, with each weight copy's problem table built once: step i runs
+    the same kernel on the same 7 problems, reading weight copy i % copies and writing outputs
+    shared by every call (as graph replays share theirs).
+
+    A timed run queues its `count` launches behind a GPU spin longer than their host enqueue
+    time, so the GPU runs them back to back: one HIP graph launch costs ~6 us of fixed time on
+    ROCm (a timed region of K graph-replayed steps measured 8.5 us + 5.69 us per step, eager
+    launches behind a spin 2.4 us + 5.69 us per step), which at the driver's K = 20 is 5% of
+    the step.  Each run checks that the host had queued every launch before the spin ended."""
+
+    def __init__(self, torch, kl, lib, xs, dev, group: int):
+        self.torch, self.m, self.group, self.count = torch, xs[0].shape[0], group, len(xs)
+        if self.count > kl.GEMV_MAX_GROUP:
+            raise ValueError(f"one grouped launch takes at most {kl.GEMV_MAX_GROUP} problems")
+        self.ys = [torch.empty(self.m, p.shape[0], dtype=torch.float16, device=xs[0].device) for p, _ in dev[0]]
+        self.tables = []
+        for weights in dev:
+            table = (kl.GemvProblem * self.count)()
+            for j, (x, (p, s), y) in enumerate(zip(xs, weights, self.ys)):
+                table[j] = kl.GemvProblem(x.data_ptr(), p.data_ptr(), s.data_ptr(), y.data_ptr(), p.shape[0],
+                                          x.shape[1])
+            self.tables.append(table)
+        self.fn, self.kl = lib.kf_int4_gemv_grouped, kl
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(self, i: int) -> None:
+        st = self.fn(self.tables[i % len(self.tables)], self.count, self.m, self.group, self.stream)
+        if st:
+            self.kl.check(st, "kf_int4_gemv_grouped")
+
+    def enqueue_us(self, n: int = 100) -> float:
+        """Host time per launch while the GPU is busy (median of 5 batches of n)."""
+        torch = self.torch
+        times = []
+        for _ in range(5):
+            torch.cuda._sleep(int((0.5 + 0.02 * n) * spin_cycles_per_ms(torch)))
+            t = time.perf_counter()
+            for i in range(n):
+                self.launch(i)
+            times.append((time.perf_counter() - t) / n * 1e6)
+            torch.cuda.synchronize()
+        return statistics.median(times)
+
+    def timed(self, count: int) -> dict:
+        """ms per step from a HIP event pair on the launching stream around exactly `count` launches,
+        between synchronize() calls, and the wall clock over the same launches minus the spin."""
+        torch = self.torch
+        enq = self.enqueue_us()
+        spin_ms = 0.5 + 2.0 * count * enq / 1e3
+        torch.cuda.synchronize()
+        g, s, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        t0 = time.perf_counter()
+        g.record()
+        torch.cuda._sleep(int(spin_ms * spin_cycles_per_ms(torch)))
+        s.record()
+        t1 = time.perf_counter()
+        for i in range(count):
+            self.launch(i)
+        queued_ms = (time.perf_counter() - t1) * 1e3
+        e.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 - g.elapsed_time(s)
+        return {"ms_per_step": s.elapsed_time(e) / count, "wall_ms_per_step": wall_ms / count,
+                "host_enqueue_us": round(enq, 2), "spin_ms": round(g.elapsed_time(s), 3),
+                "queued_ms": round(queued_ms, 3), "covered": queued_ms < g.elapsed_time(s)}
+
+
 def reference_protocol(torch, fn, copies: int, iters: int = 50, warmup: int = 10,
                        min_warmup_ms: float = 100.0) -> dict:
     """The reference's per-call timing (kernelforge/bench_utils.py:114-185), restated: warm up for at
@@ -647,27 +722,42 @@ def main() -> int:
             single(r, nm)
 
     # --- the timed step (value): one grouped launch over the 7 linears --------------------------
-    # Every graph the warm-up and the timed run replay is captured first; the timed region then
-    # only replays (W warm-up steps, then exactly K steps between synchronize() calls), timed by
-    # a HIP event pair on the launching stream, with the host's wall clock beside it.
+    # W warm-up steps, then exactly K steps between synchronize() calls, timed by a HIP event pair
+    # on the launching stream, with the host's wall clock beside it.  Up to BOUND_MAX_STEPS the K
+    # steps are eager launches of the op's C-ABI call queued behind a spin (BoundSteps: no graph
+    # launch's fixed cost in a short timed region); beyond, replays of graphs all captured before
+    # the timed region (GraphSteps: the fixed cost is spread over many steps, and the GPU's
+    # command queue need not hold every launch at once).  Both timings are reported.
     log(f"{copies} weight copies ({copies * set_bytes / 2**20:.0f} MiB); warmup {args.warmup} steps")
     main_steps = GraphSteps(torch, step_grouped, copies)
     main_steps.prepare(args.warmup)
     main_steps.prepare(args.steps)
     main_steps.prepare(copies)
     main_steps.run(args.warmup)
+    bound = BoundSteps(torch, kl, lib, xs, dev, GROUP)
     # The reference's warm-up rule on top of the W requested steps (kernelforge/bench_utils.py:
     # 114-185: at least 10 calls and 100 ms), in whole passes over the weight copies, so a short
     # run (the driver's --steps 20 --warmup 5) times a warm GPU as a long one does.
     warm_steps, t_warm = args.warmup, time.perf_counter()
     while warm_steps < args.warmup + 10 or time.perf_counter() - t_warm < 0.1:
         main_steps.run(copies)
+        for i in range(copies):
+            bound.launch(i)
         torch.cuda.synchronize()
-        warm_steps += copies
-    ms_per_step, wall_ms_per_step = main_steps.timed(args.steps)
+        warm_steps += 2 * copies
+    graph_ms, graph_wall_ms = main_steps.timed(args.steps)
+    bound_timing = None
+    if args.steps <= BOUND_MAX_STEPS:
+        bound_timing = bound.timed(args.steps)
+        if not bound_timing["covered"]:  # the host fell behind the spin once: one retry, then graphs
+            bound_timing = bound.timed(args.steps)
+    if bound_timing and bound_timing["covered"]:
+        ms_per_step, wall_ms_per_step, timed_by = bound_timing["ms_per_step"], bound_timing["wall_ms_per_step"], "bound"
+    else:
+        ms_per_step, wall_ms_per_step, timed_by = graph_ms, graph_wall_ms, "graph"
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"grouped 7-layer step {ms_per_step * 1e3:.3f} us (events; wall clock {wall_ms_per_step * 1e3:.3f} us) "
-        f"-> {value:.0f} GB/s")
+    log(f"grouped 7-layer step {ms_per_step * 1e3:.3f} us ({timed_by} launches, events; wall clock "
+        f"{wall_ms_per_step * 1e3:.3f} us; graph replays {graph_ms * 1e3:.3f} us) -> {value:.0f} GB/s")
 
     # --- roofline of the dominant kernel (the grouped GEMV: one launch per step) ----------------
     # achieved: the timed region's own event average (one launch per step); a longer event run
@@ -804,10 +894,17 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "tinyllama_7_linears_m1_g128", "shapes_NxK": [[n, k] for _, n, k in TL_LAYERS],
                    "group_size": GROUP, "bytes_per_step": step_bytes, "weight_copies_rotated": copies,
-                   "step": "one int4_linear_grouped launch over the 7 independent linears",
-                   "graph_captured": True},
-        "timer": {"ms_per_step": "HIP event pair on the launching stream around the K replayed steps, "
-                                 "between synchronize() calls; every graph captured before the timed region",
+                   "step": "one int4_linear_grouped launch (its C-ABI call kf_int4_gemv_grouped) over the 7 "
+                           "independent linears",
+                   "launched_as": timed_by},
+        "timer": {"ms_per_step": "HIP event pair on the launching stream around exactly K steps, between "
+                                 "synchronize() calls: K <= %d eager launches of kf_int4_gemv_grouped queued behind "
+                                 "a GPU spin longer than their host enqueue (bound), else replays of graphs "
+                                 "captured before the timed region (graph)" % BOUND_MAX_STEPS,
+                  "launched_as": timed_by,
+                  "bound": bound_timing,
+                  "graph_ms_per_step": round(graph_ms, 6),
+                  "graph_wall_ms_per_step": round(graph_wall_ms, 6),
                   "wall_ms_per_step": round(wall_ms_per_step, 6),
                   "warmup_steps_run": warm_steps,
                   "warmup_rule": "the W requested steps, then whole passes over the weight copies until at "
