@@ -366,10 +366,9 @@ def int4_gemv_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scales
         raise ValueError(f"int4_gemv handles M in [1, 8], got M={m}")
     lib = _lib.load()
     dev = xs[0].device
-    # One allocation for all outputs (row-major [m, N_i] views of consecutive slices).
+    # One tensor per output: the registered grouped op may not return outputs that alias each other.
     ns = [p.shape[0] for p in packed]
-    ys = [y.view(m, n) for y, n in zip(torch.empty(m * sum(ns), dtype=torch.float16, device=dev)
-                                        .split([m * n for n in ns]), ns)]
+    ys = [torch.empty(m, n, dtype=torch.float16, device=dev) for n in ns]
     problem = _lib.GemvProblem
     with _on(dev):
         stream = _stream_ptr(dev)
