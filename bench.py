@@ -238,6 +238,8 @@ def e2e_decode(torch, prompt_len: int = 16, new_tokens: int = 128) -> dict:
         tps, toks = run(model)
         out[f"{label}_tok_s"] = round(tps, 1)
         out[f"{label}_first_tokens"] = toks[:8].tolist()
+        if label == "int4_fused":
+            out["mfma16_copies"] = mfma16_copy_report(model)
         del model
         torch.cuda.empty_cache()
     with torch.device(dev):
@@ -247,6 +249,29 @@ def e2e_decode(torch, prompt_len: int = 16, new_tokens: int = 128) -> dict:
     del fp16
     torch.cuda.empty_cache()
     return out
+
+
+def mfma16_copy_report(model) -> dict:
+    """Device memory of the MFMA-16 weight copies int4_gemm attached to the model's INT4 weights
+    (built on the first skinny-kernel call per weight: here the 16-token prefill), against the
+    INT4 weights themselves."""
+    from kernelforge import ops
+
+    storages, copies, copy_bytes = {}, 0, 0
+    for mod in model.modules():
+        packed, scales = getattr(mod, "packed", None), getattr(mod, "scales", None)
+        if packed is None or scales is None:
+            continue
+        for t in (packed, scales):  # a fused module's parts are views of its buffers: count storages
+            storages[t.untyped_storage().data_ptr()] = t.untyped_storage().nbytes()
+        cached = getattr(packed, ops._MFMA16_ATTR, None)
+        if cached is not None:
+            copies += 1
+            copy_bytes += cached[1].numel() * 4 + cached[2].numel() * 2
+    int4 = sum(storages.values())
+    return {"weights_with_copy": copies, "copy_bytes": copy_bytes, "int4_weight_bytes": int4,
+            "copy_over_int4_weights": round(copy_bytes / int4, 3) if int4 else None,
+            "note": "second layout of each weight the skinny kernel has run on (ops.MFMA16_CACHE)"}
 
 
 def log(msg: str) -> None:

@@ -98,6 +98,13 @@ class FusedInt4Linear(nn.Module):
         self.splits = [p.out_features for p in parts]
         self.register_buffer("packed", torch.cat([p.packed for p in parts], dim=0).contiguous())
         self.register_buffer("scales", torch.cat([p.scales for p in parts], dim=0).contiguous())
+        # The parts keep working on the same bytes: their buffers become row slices (contiguous
+        # views) of the concatenated ones, so fusing holds no second copy of the weights.
+        off = 0
+        for p in parts:
+            p.packed = self.packed[off:off + p.out_features]
+            p.scales = self.scales[off:off + p.out_features]
+            off += p.out_features
 
     def forward(self, x: torch.Tensor) -> list[torch.Tensor]:
         return list(torch.split(self.forward_concat(x), self.splits, dim=-1))
