@@ -914,7 +914,7 @@ constexpr int kMaxSplits = 12;  // the largest split count the fit was measured 
 GemmPlan plan_for(int K, int tile, int splits) {
   GemmPlan p;
   p.skinny = false;
-  p.sk = SkinnyPlan{0, 0, 0};
+  p.sk = SkinnyPlan{0, 0, 0, false, 0};
   p.tile = tile;
   p.block_m = kTiles[tile].bm;
   p.block_n = kTiles[tile].bn;

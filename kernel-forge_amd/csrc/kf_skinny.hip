@@ -17,8 +17,13 @@
 //     for both operands: B = dequant8(word t) of its column, A = 8 consecutive x values of
 //     row (16*mt + l%16).  Since A and B agree on which k each (lane group, slot) holds, the
 //     MFMA sums exactly the 128 k of the super-step.
-//   * Weight loads of UU super-steps are issued before their math (one round trip per pass);
-//     x comes from L2.
+//   * Weight loads of UU super-steps are issued before their math (one round trip per pass).
+//   * x: a wavefront's fragments are rows 0..15 (x 16 B each) of its own k range, and every
+//     workgroup needs all of x, so per-lane loads from L2 moved 4x the weight bytes through the
+//     load path (a timing-only copy without them ran 30-40% faster).  When the plan allows
+//     (SkinnyPlan::x_lds), each wavefront first copies its k range of the M real rows into a
+//     region of LDS of its own with LDS-DMA (no registers, no duplicate rows), waits for it with
+//     its first weights, and reads the fragments from there; otherwise the lanes load x from L2.
 //   * The KS partial 16 x 16*MT tiles are summed in fixed wavefront order through LDS
 //     (deterministic) and written as fp16.  Rows past M read row M-1 and are never stored;
 //     columns past N read row N-1 and are never stored.
@@ -34,11 +39,22 @@
 namespace kf {
 namespace {
 
-template <int MT, int U, bool BLOCKED>
+__device__ __forceinline__ void dma_16B(uint32_t lds, const void* src) {
+  asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(lds), "v"(src) : "memory");
+}
+
+// LDS layout of the x copy (XL): wavefront w's region holds rows 0..M-1 of its k range, each row
+// `cpr` 16-byte chunk slots (16 per super-step, for the longest range of any wavefront); chunk c of
+// row r sits at slot c ^ (r & 15), so the 16 lanes of a fragment-read phase (16 rows, one chunk)
+// hit 16 different bank groups.  Regions are whole LDS-DMA instructions (64 slots) long.
+__host__ __device__ inline int skinny_x_cpr(int nss, int ks) { return 16 * ((nss + ks - 1) / ks); }
+__host__ __device__ inline int skinny_x_region_slots(int M, int cpr) { return (M * cpr + 63) & ~63; }
+
+template <int MT, int U, bool BLOCKED, bool XL>
 __global__ __launch_bounds__(1024) void skinny_kernel(const half_t* __restrict__ x, const uint32_t* __restrict__ packed,
                                                       const half_t* __restrict__ scales, half_t* __restrict__ y,
                                                       int M, int N, int K, int log2_group) {
-  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][MT * 256]
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [KS][MT * 256], then (XL) the x regions
   const int ks_waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -66,6 +82,22 @@ __global__ __launch_bounds__(1024) void skinny_kernel(const half_t* __restrict__
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  // XL: this wavefront's k range of x rows 0..M-1 into its LDS region (see skinny_x_cpr).  Slots
+  // past the last row (the region's rounding) re-load row M-1; chunks past K re-load the last one.
+  const int cpr = skinny_x_cpr(nss, ks_waves);
+  const unsigned char* xw = reinterpret_cast<const unsigned char*>(red) + ks_waves * MT * 1024 +
+                            wave * skinny_x_region_slots(M, cpr) * 16;
+  if constexpr (XL) {
+    const uint32_t base = (uint32_t)(uintptr_t)xw;
+    const int slots = skinny_x_region_slots(M, cpr);
+    for (int i0 = 0; i0 < slots; i0 += 64) {
+      const int q = i0 + lane;
+      const int r = min(q / cpr, M - 1), p = q % cpr;
+      const int c = min(16 * ss_begin + (p ^ (r & 15)), (K >> 3) - 1);
+      dma_16B(__builtin_amdgcn_readfirstlane(base + 16 * i0), x + (size_t)r * K + 8 * c);
+    }
+  }
+
   for (int ss = ss_begin; ss < ss_end; ss += U) {
     u32x4 wv[U];
     half_t sv[U];
@@ -75,10 +107,28 @@ __global__ __launch_bounds__(1024) void skinny_kernel(const half_t* __restrict__
       const int s = min(ss + u, ss_end - 1);  // in range; repeats are masked below
       wv[u] = load_u32x4_stream(wrow + W_STEP * s);
       sv[u] = srow[S_STEP * ((128 * s + 32 * g) >> log2_group)];
+      if constexpr (!XL) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) xa[u][mt][t] = *reinterpret_cast<const half8_t*>(xrow[mt] + 128 * s + 8 * t);
+          for (int t = 0; t < 4; ++t) xa[u][mt][t] = *reinterpret_cast<const half8_t*>(xrow[mt] + 128 * s + 8 * t);
+      }
+    }
+    if constexpr (XL) {
+      // The x copy (issued before the first pass) and this pass's weights have landed; the copy
+      // is not tracked by the compiler, hence the explicit wait.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int p0 = 16 * (min(ss + u, ss_end - 1) - ss_begin) + 4 * g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int r = min(16 * mt + col, M - 1);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            xa[u][mt][t] = *reinterpret_cast<const half8_t*>(xw + 16 * (r * cpr + ((p0 + t) ^ (r & 15))));
+        }
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -114,13 +164,12 @@ __global__ __launch_bounds__(1024) void skinny_kernel(const half_t* __restrict__
 
 typedef void (*SkinnyFn)(const half_t*, const uint32_t*, const half_t*, half_t*, int, int, int, int);
 
-template <bool B>
+template <bool B, bool XL>
 SkinnyFn skinny_fn(int mt, int u) {
   switch (mt) {
-    case 1: return u >= 4 ? skinny_kernel<1, 4, B> : (u == 2 ? skinny_kernel<1, 2, B> : skinny_kernel<1, 1, B>);
-    case 2: return u >= 2 ? skinny_kernel<2, 2, B> : skinny_kernel<2, 1, B>;
-    case 3: return skinny_kernel<3, 1, B>;
-    default: return skinny_kernel<4, 1, B>;
+    case 1:
+      return u >= 4 ? skinny_kernel<1, 4, B, XL> : (u == 2 ? skinny_kernel<1, 2, B, XL> : skinny_kernel<1, 1, B, XL>);
+    default: return u >= 2 ? skinny_kernel<2, 2, B, XL> : skinny_kernel<2, 1, B, XL>;
   }
 }
 
@@ -155,8 +204,6 @@ __global__ __launch_bounds__(256) void reorder_mfma16_kernel(const u32x4* __rest
 }  // namespace
 
 SkinnyPlan skinny_plan(int M, int N, int K, int cu_count) {
-  (void)N;
-  (void)cu_count;
   SkinnyPlan p;
   p.m_tiles = ceil_div(M, 16);
   // The K split depends on K (and M) only, never on N: a column's result is then the same
@@ -176,14 +223,37 @@ SkinnyPlan skinny_plan(int M, int N, int K, int cu_count) {
   int u = per_wave < u_max ? per_wave : u_max;
   if (u == 3) u = 2;
   p.unroll = u < 1 ? 1 : u;
+  // x through LDS (row-major weights only, see skinny_launch) when its copy fits, the grid still
+  // runs in one round at the workgroups per CU that LDS then allows (Qwen2.5 gate/up at M = 16,
+  // 560 workgroups of 55 KiB, would need two: 5% slower), and K >= 2048 or the grid has at least
+  // one workgroup per CU.  Measured on the public layout, M = 4..32: TinyLlama's 4 layer shapes
+  // 5-20% faster, Qwen2.5 gate/up and down up to 10% faster, Qwen2.5 q/o and k/v (K = 1536, 96 and
+  // 16 workgroups) 3-9% slower with the copy, hence the last condition.
+  const int red = ks * p.m_tiles * 1024;
+  const long xb = (long)ks * skinny_x_region_slots(M, skinny_x_cpr(nss, ks)) * 16;
+  const long lds = red + xb;
+  const long cus = cu_count > 0 ? cu_count : 256;
+  const long wgs = ceil_div(N, 16);
+  p.x_lds = lds <= kSkinnyMaxLds && wgs <= cus * (kSkinnyMaxLds / lds) && (K >= 2048 || wgs >= cus);
+  p.lds_bytes = (int)(p.x_lds ? lds : red);
   return p;
 }
 
 hipError_t skinny_launch(const SkinnyPlan& p, const void* x, const void* packed, const void* scales, void* y, int M,
                          int N, int K, int group_size, bool blocked, hipStream_t stream) {
   const int log2_group = group_size == 128 ? 7 : 6;
-  const size_t lds = (size_t)p.ks_waves * p.m_tiles * 256 * sizeof(float);
-  const SkinnyFn fn = blocked ? skinny_fn<true>(p.m_tiles, p.unroll) : skinny_fn<false>(p.m_tiles, p.unroll);
+  // The x copy pays only with the row-major weights: with the MFMA-16 blocks the weight loads are
+  // contiguous and the lanes' x loads are not what the kernel waits on (M = 4..16: 5% slower).
+  const bool xl = p.x_lds && !blocked;
+  const size_t lds = xl ? (size_t)p.lds_bytes : (size_t)p.ks_waves * p.m_tiles * 1024;
+  const SkinnyFn fn = blocked ? skinny_fn<true, false>(p.m_tiles, p.unroll)
+                              : (xl ? skinny_fn<false, true>(p.m_tiles, p.unroll)
+                                    : skinny_fn<false, false>(p.m_tiles, p.unroll));
+  if (lds > 65536) {  // dynamic LDS beyond 64 KiB is opted into per kernel
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kSkinnyMaxLds);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(fn, dim3(ceil_div(N, 16)), dim3(64 * p.ks_waves), lds, stream,
                      static_cast<const half_t*>(x), static_cast<const uint32_t*>(packed),
                      static_cast<const half_t*>(scales), static_cast<half_t*>(y), M, N, K, log2_group);

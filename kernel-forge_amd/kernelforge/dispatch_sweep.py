@@ -111,11 +111,16 @@ def main() -> None:
     ap.add_argument("--shapes", default=",".join(SHAPES))
     ap.add_argument("--out", default=None)
     ap.add_argument("--fp16", action="store_true", help="also time F.linear on fp16 weights (hipBLASLt)")
+    ap.add_argument("--no-mfma16", action="store_true",
+                    help="int4_gemm on the public weight layout only (ops.MFMA16_CACHE = False)")
     args = ap.parse_args()
+    if args.no_mfma16:
+        ops.MFMA16_CACHE = False
     ms = [int(v) for v in args.ms.split(",")]
     shapes = {s: SHAPES[s] for s in args.shapes.split(",")}
     res = sweep(ms, shapes, fp16=args.fp16)
     out = {"results_us": res, "gemv_max_m": crossover(res, ms), "current_GEMV_MAX_M": ops.GEMV_MAX_M,
+           "mfma16_cache": ops.MFMA16_CACHE,
            "device": torch.cuda.get_device_name(0)}
     print(json.dumps({"gemv_max_m": out["gemv_max_m"]}), flush=True)
     if args.out:
