@@ -95,7 +95,8 @@ def test_plans_without_split_k(m, n, k):
 def test_refuses_a_plan_larger_than_the_scratch():
     """A long-K problem on few tiles splits K many ways: its partials exceed the scratch, so the
     entry point returns KF_ERR_WORKSPACE before launching (y stays untouched)."""
-    for m, n, k in [(1024, 1024, 65536), (512, 2048, 65536), (2048, 1024, 65536)]:
+    # On 256 CUs: 128 x 128 tiles split 3 ways (60 MiB of partials), 5 ways (60 MiB), 7 ways (63 MiB).
+    for m, n, k in [(2048, 2560, 16384), (1536, 2048, 32768), (1536, 1536, 65536)]:
         if _plan(m, n, k)[2] > _lib.KF_NOALLOC_SCRATCH_BYTES:
             break
     else:
