@@ -118,16 +118,17 @@ constexpr float kMinus8TwoPowMinus24 = -4.76837158203125e-07f;  // -8 * 2^-24
 // The workgroup's LDS copy of x (dynamic shared memory, sized per launch; plan.x_lds only).
 extern __shared__ __attribute__((aligned(1024))) u32x4 gemv_x_lds[];
 
-// Copies x (n16 16-byte pieces) into gemv_x_lds with LDS-DMA: wavefront w of the workgroup
-// moves 1 KiB blocks w, w + 4, ... straight from global memory to LDS, no registers involved.
+// Copies x (n16 16-byte pieces) into gemv_x_lds with LDS-DMA: wavefront w of a WPB-wavefront
+// workgroup moves 1 KiB blocks w, w + WPB, ... straight from global memory to LDS, no registers.
 // Lanes past the end re-read the last piece into the tail of the last block (inside the
 // allocation, which the launcher rounds up to whole 1 KiB blocks).  Completion is awaited
 // with vmcnt in gemv_pass.  `off`: byte offset of the destination in the LDS allocation.
+template <int WPB = kGemvWavesPerBlock>
 __device__ __forceinline__ void stage_x_lds(const half_t* x, int n16, int lane, uint32_t off = 0) {
   const uint32_t base = (uint32_t)(uintptr_t)gemv_x_lds + off;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blocks = (n16 + 63) >> 6;
-  for (int b = wave; b < blocks; b += kGemvWavesPerBlock) {
+  for (int b = wave; b < blocks; b += WPB) {
     const int idx = min(64 * b + lane, n16 - 1);
     asm volatile("global_load_lds_dwordx4 %1, off" ::"{m0}"(__builtin_amdgcn_readfirstlane(base + 1024u * b)),
                  "v"(x + 8 * idx)
@@ -165,11 +166,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 // [2 xb, 3 xb) the second input (RMSNorm weight, up).  Writing x to its own region lets every
 // wavefront read the whole input row while others already write, so one barrier suffices.
 //   RMSNorm: x = fp16((x * rsqrt(sum(x^2) / K + eps)) * w); every wavefront sums the whole row in
-//            fp32 in the same order (per lane, then across the wavefront), so all agree.
+//            the same order (per lane with v_dot2_f32_f16 on pairs, fp32, then across the
+//            wavefront), so all agree.
 //   SwiGLU:  x = fp16(float(fp16(silu(gate))) * up), silu(g) = g * rcp(1 + exp(-g)) with the
 //            hardware exp and reciprocal (about 1 ulp of fp32 each, far below the fp16 rounding
 //            that follows), and torch's two fp16 roundings of silu(gate) * up.
-template <int PRO>
+template <int PRO, int WPB>
 __device__ __forceinline__ void x_prologue(int K, float eps) {
   const int tid = threadIdx.x;
   const int k8 = K >> 3;
@@ -177,18 +179,18 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
   const u32x4* in = gemv_x_lds + xb;
   const u32x4* in2 = gemv_x_lds + 2 * xb;
   if constexpr (PRO == kGemvProRmsNorm) {
-    float ss = 0.0f;
+    // Squares of pairs with dot2 (products exact in fp32): a quarter of the VALU of converting and
+    // multiplying each element, and every wavefront of every workgroup repeats this sum.
+    float s0 = 0.0f, s1 = 0.0f;
     for (int p = tid & 63; p < k8; p += 64) {
       const u32x4 v = in[p];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const half2_t h = bit_cast<half2_t>(v[j]);
-        ss = fmaf((float)h[0], (float)h[0], ss);
-        ss = fmaf((float)h[1], (float)h[1], ss);
-      }
+      s0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(v[0]), bit_cast<half2_t>(v[0]), s0, false);
+      s1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(v[1]), bit_cast<half2_t>(v[1]), s1, false);
+      s0 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(v[2]), bit_cast<half2_t>(v[2]), s0, false);
+      s1 = __builtin_amdgcn_fdot2(bit_cast<half2_t>(v[3]), bit_cast<half2_t>(v[3]), s1, false);
     }
-    const float rstd = rsqrtf(wave_sum(ss) / (float)K + eps);
-    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
+    const float rstd = rsqrtf(wave_sum(s0 + s1) / (float)K + eps);
+    for (int p = tid; p < k8; p += 64 * WPB) {
       const u32x4 v = in[p], g = in2[p];
       u32x4 o;
 #pragma unroll
@@ -201,7 +203,7 @@ __device__ __forceinline__ void x_prologue(int K, float eps) {
     }
   } else {
     static_assert(PRO == kGemvProSwiGLU, "prologue kind");
-    for (int p = tid; p < k8; p += 64 * kGemvWavesPerBlock) {
+    for (int p = tid; p < k8; p += 64 * WPB) {
       const u32x4 gv = in[p], uv = in2[p];
       u32x4 o;
 #pragma unroll
@@ -275,7 +277,7 @@ struct RowSet {
 // vector-memory loads issued after the copy are this pass's UU * R weight and UU * R scale
 // loads, so vmcnt(2 * UU * R) means the copy has landed, and the barrier makes every
 // wavefront's share visible to all.
-template <int M, int R, int UU, bool XLDS, int PRO = kGemvProNone>
+template <int M, int R, int UU, bool XLDS, int PRO = kGemvProNone, int WPB = kGemvWavesPerBlock>
 __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane, float (&acc)[M][R], bool first) {
   constexpr int XM = XPrefetch<M>::value;
   u32x4 wv[UU][R];
@@ -304,7 +306,7 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
     if (first) {
       wait_vmcnt<2 * UU * R>();
       __syncthreads();
-      if constexpr (PRO != kGemvProNone) x_prologue<PRO>(rs.K, rs.eps);
+      if constexpr (PRO != kGemvProNone) x_prologue<PRO, WPB>(rs.K, rs.eps);
     }
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
@@ -364,7 +366,8 @@ __device__ __forceinline__ void gemv_pass(const RowSet<R>& rs, int cb, int lane,
 // Rows row0 .. row0 + R - 1 of one problem (the body both entry kernels share, so a problem
 // gives the same bits whichever kernel runs it).  Rows past N are clamped to N - 1 for
 // loading and never stored.
-template <int M, int R, int UMAX, bool XLDS, int PRO = kGemvProNone, bool ROPE = false>
+template <int M, int R, int UMAX, bool XLDS, int PRO = kGemvProNone, bool ROPE = false,
+          int WPB = kGemvWavesPerBlock>
 __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packed, const half_t* scales,
                                           half_t* y, int N, int K, int scale_shift, int row0, int lane,
                                           const half_t* res = nullptr, const half_t* aux = nullptr,
@@ -375,8 +378,8 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
     if constexpr (PRO == kGemvProNone) {
       stage_x_lds(x, (M * K) >> 3, lane);
     } else {  // the row and the second input go past the x region, which the prologue writes
-      stage_x_lds(x, K >> 3, lane, x_row_lds_bytes(K));
-      stage_x_lds(aux, K >> 3, lane, 2 * x_row_lds_bytes(K));
+      stage_x_lds<WPB>(x, K >> 3, lane, x_row_lds_bytes(K));
+      stage_x_lds<WPB>(aux, K >> 3, lane, 2 * x_row_lds_bytes(K));
     }
     // The first pass counts its own weight and scale loads as the only ones issued after the
     // copy.  Loads through __restrict__ arguments could legally be moved past the copy's
@@ -413,16 +416,16 @@ __device__ __forceinline__ void gemv_rows(const half_t* x, const uint32_t* packe
     const int left = rs.chunks - cb;  // uniform
     const bool first = cb == 0;
     if (UMAX >= 4 && left > 192) {
-      gemv_pass<M, R, (UMAX >= 4 ? 4 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 4 ? 4 : 1), XLDS, PRO, WPB>(rs, cb, lane, acc, first);
       cb += 256;
     } else if (UMAX >= 3 && left > 128) {
-      gemv_pass<M, R, (UMAX >= 3 ? 3 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 3 ? 3 : 1), XLDS, PRO, WPB>(rs, cb, lane, acc, first);
       cb += 192;
     } else if (UMAX >= 2 && left > 64) {
-      gemv_pass<M, R, (UMAX >= 2 ? 2 : 1), XLDS, PRO>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, (UMAX >= 2 ? 2 : 1), XLDS, PRO, WPB>(rs, cb, lane, acc, first);
       cb += 128;
     } else {
-      gemv_pass<M, R, 1, XLDS, PRO>(rs, cb, lane, acc, first);
+      gemv_pass<M, R, 1, XLDS, PRO, WPB>(rs, cb, lane, acc, first);
       cb += 64;
     }
   }
@@ -675,28 +678,31 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_kernel(const hal
 
 // One problem at M = 1 with a prologue on x (GemvPrologue) and/or a residual: gemv_kernel with
 // x in LDS, whose copy the prologue transforms before the first product.  y may alias res.
+// Workgroups of gemv_fused_waves_per_block(PRO) wavefronts.
 template <int R, int UMAX, int PRO>
-__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_fused_kernel(
+__global__ __launch_bounds__(64 * gemv_fused_waves_per_block(PRO)) void gemv_fused_kernel(
     const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
     int N, int K, int scale_shift, const half_t* res, const half_t* __restrict__ aux, float eps) {
+  constexpr int WPB = gemv_fused_waves_per_block(PRO);
   const int lane = threadIdx.x & 63;
   const int lb = xcd_run_block();
-  if (lb * kGemvWavesPerBlock * R >= N) return;  // a padded workgroup: all of its wavefronts leave
-  const int row0 = (lb * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
-  gemv_rows<1, R, UMAX, true, PRO>(x, packed, scales, y, N, K, scale_shift, row0, lane, res, aux, eps);
+  if (lb * WPB * R >= N) return;  // a padded workgroup: all of its wavefronts leave
+  const int row0 = (lb * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  gemv_rows<1, R, UMAX, true, PRO, false, WPB>(x, packed, scales, y, N, K, scale_shift, row0, lane, res, aux, eps);
 }
 
 // The q|k|v decode GEMV with the RoPE + KV-cache epilogue (GemvRope), optionally an RMSNorm
 // prologue.  Wavefront w < (heads + kv_heads) * d / 2 owns dims j, j + d / 2 of head w / (d / 2);
-// the rest own two consecutive v rows.
+// the rest own two consecutive v rows.  Workgroups of gemv_fused_waves_per_block(PRO) wavefronts.
 template <int UMAX, int PRO>
-__global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_qkv_rope_kernel(
+__global__ __launch_bounds__(64 * gemv_fused_waves_per_block(PRO)) void gemv_qkv_rope_kernel(
     const half_t* __restrict__ x, const uint32_t* __restrict__ packed, const half_t* __restrict__ scales, half_t* y,
     int N, int K, int scale_shift, const half_t* __restrict__ aux, float eps, const GemvRope rope) {
+  constexpr int WPB = gemv_fused_waves_per_block(PRO);
   const int lane = threadIdx.x & 63;
   const int lb = xcd_run_block();
-  if (lb * kGemvWavesPerBlock * 2 >= N) return;  // a padded workgroup: all of its wavefronts leave
-  const int w = lb * kGemvWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (lb * WPB * 2 >= N) return;  // a padded workgroup: all of its wavefronts leave
+  const int w = lb * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half_d = rope.head_dim >> 1;
   const int nwr = (rope.heads + rope.kv_heads) * half_d;
   int row0, step;
@@ -708,8 +714,8 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_qkv_rope_kernel(
     row0 = 2 * nwr + 2 * (w - nwr);
     step = 1;
   }
-  gemv_rows<1, 2, UMAX, true, PRO, true>(x, packed, scales, y, N, K, scale_shift, row0, lane, nullptr, aux, eps,
-                                         step, &rope);
+  gemv_rows<1, 2, UMAX, true, PRO, true, WPB>(x, packed, scales, y, N, K, scale_shift, row0, lane, nullptr, aux,
+                                              eps, step, &rope);
 }
 
 // Several problems.  b1 .. b8: first global wavefront of problems 1 .. 8 (ascending; the
@@ -1034,10 +1040,11 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
 hipError_t gemv_qkv_rope_launch(const GemvProblem& q, const GemvFused& f, const GemvRope& rope, int unroll,
                                 int group_size, hipStream_t stream) {
   const int shift = group_size == 128 ? 2 : 1;  // log2(G / 32)
-  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, 2), kGemvWavesPerBlock));
+  const int wpb = gemv_fused_waves_per_block(f.prologue);
+  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, 2), wpb));
   const GemvRopeFn fn = f.prologue == kGemvProRmsNorm ? pick_rope_u<kGemvProRmsNorm>(unroll)
                                                       : pick_rope_u<kGemvProNone>(unroll);
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * kGemvWavesPerBlock), fused_lds_bytes(q.K, f.prologue), stream,
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * wpb), fused_lds_bytes(q.K, f.prologue), stream,
                      static_cast<const half_t*>(q.x), static_cast<const uint32_t*>(q.packed),
                      static_cast<const half_t*>(q.scales), static_cast<half_t*>(q.y), q.N, q.K, shift,
                      static_cast<const half_t*>(f.aux), f.eps, rope);
@@ -1053,8 +1060,9 @@ hipError_t gemv_fused_launch(const GemvPlan& plan, const GemvProblem& q, const G
   // third row's sums are added in the same order, so the bits do not change.
   int rows = plan.rows_per_wave == 1 ? 1 : 2;
   if (rows == 2 && f.prologue != kGemvProNone && q.N >= 8192) rows = 3;
-  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, rows), kGemvWavesPerBlock));
-  hipLaunchKernelGGL(pick_fused(f.prologue, rows, plan.unroll), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
+  const int wpb = gemv_fused_waves_per_block(f.prologue);
+  const int blocks = xcd_grid(ceil_div(ceil_div(q.N, rows), wpb));
+  hipLaunchKernelGGL(pick_fused(f.prologue, rows, plan.unroll), dim3(blocks), dim3(64 * wpb),
                      fused_lds_bytes(q.K, f.prologue), stream, static_cast<const half_t*>(q.x),
                      static_cast<const uint32_t*>(q.packed), static_cast<const half_t*>(q.scales),
                      static_cast<half_t*>(q.y), q.N, q.K, shift, static_cast<const half_t*>(f.residual),

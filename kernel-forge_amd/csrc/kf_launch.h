@@ -96,6 +96,16 @@ enum GemvPrologue {
   kGemvProSwiGLU = 2,   // fp16(fp16(silu(gate)) * up) (x: gate [K], aux: up [K])
 };
 constexpr int kGemvFusedMaxK = kGemvMaxLdsX / 2;  // x of the one row fits the LDS budget
+// Workgroup size of the fused launches.  With a prologue every workgroup copies two input rows
+// into LDS and transforms them before its first product; eight wavefronts per workgroup halve
+// those copies and that work (MI355X, TinyLlama decode shapes: gate|up with RMSNorm
+// 5.16 -> 4.93 us, down with SwiGLU and residual 4.26 -> 3.51, q|k|v with RMSNorm and RoPE
+// 3.89 -> 3.48; sixteen are slower than four).  Without a prologue the plain GEMV's four stay
+// faster.
+constexpr int kGemvWavesPerBlockPrologue = 8;
+constexpr int gemv_fused_waves_per_block(int prologue) {
+  return prologue == kGemvProNone ? kGemvWavesPerBlock : kGemvWavesPerBlockPrologue;
+}
 struct GemvFused {
   int prologue;          // GemvPrologue
   const void* aux;       // prologue input (see GemvPrologue), else nullptr
