@@ -28,7 +28,8 @@ Protocol
   is excluded.  K <= 512: the K steps are eager launches of the op's C-ABI call
   with each weight copy's problem table built once, queued behind a spin longer
   than their enqueue (a HIP graph launch has ~6 us of fixed cost on ROCm, 5% of
-  the step at K = 20); larger K: replays of HIP graphs (R steps per graph, as in
+  the step at K = 20), after two untimed runs of that same pattern (the first
+  two in a process read slow); larger K: replays of HIP graphs (R steps per graph, as in
   the reference's CUDA-graph decode), all captured before timing.  The graph
   timing of the same K and the host wall clock are reported beside it.
 * roofline: the dominant kernel is the grouped GEMV (the whole step, one launch
@@ -386,6 +387,7 @@ class GraphSteps:
 
 
 BOUND_MAX_STEPS = 512  # longest timed region run as eager launches behind one spin (BoundSteps)
+BOUND_REHEARSALS = 2   # untimed runs of that region's pattern before the timed one
 
 
 class BoundSteps:
@@ -773,6 +775,11 @@ def main() -> int:
     graph_ms, graph_wall_ms = main_steps.timed(args.steps)
     bound_timing = None
     if args.steps <= BOUND_MAX_STEPS:
+        # Two untimed rehearsals of the timed pattern (spin, then K queued launches): the first
+        # two such regions of a process read 0.1-0.3 us per step slow on MI355X, later ones do not.
+        for _ in range(BOUND_REHEARSALS):
+            bound.timed(args.steps)
+            warm_steps += args.steps
         bound_timing = bound.timed(args.steps)
         if not bound_timing["covered"]:  # the host fell behind the spin once: one retry, then graphs
             bound_timing = bound.timed(args.steps)
@@ -933,7 +940,8 @@ def main() -> int:
                   "wall_ms_per_step": round(wall_ms_per_step, 6),
                   "warmup_steps_run": warm_steps,
                   "warmup_rule": "the W requested steps, then whole passes over the weight copies until at "
-                                 "least W + 10 steps and 100 ms (the reference's rule)"},
+                                 "least W + 10 steps and 100 ms (the reference's rule); for bound timing also "
+                                 f"{BOUND_REHEARSALS} untimed runs of the timed region's pattern"},
         "pct_of_measured_copy": round(100 * value / ceil["hbm_copy_gbps"], 1),
         "pct_of_measured_read": round(100 * value / ceil["hbm_read_gbps"], 1),
         "reference_pct_of_copy_on_its_gpu": REFERENCE_PCT_OF_COPY,
