@@ -88,7 +88,7 @@ int kf_int4_gemv_grouped(const kf_gemv_problem* problems, int count, int M, int 
  * GPU with cu_count compute units (<= 0: the current device's).  *kernel: KF_GEMV_KERNEL_*;
  * rows[i] (count entries): output rows per wavefront of problem i (1, 2 or 3), KF_GEMV_FLAT + F
  * (F rows of K = 1024 or 1536 per wavefront, their chunks packed into full 64-lane loads) or
- * KF_GEMV_DEEP (one row per wavefront, up to four 64-chunk blocks per memory round trip);
+ * KF_GEMV_DEEP (two long rows per wavefront, five 64-chunk blocks per memory round trip);
  * *unroll: 64-chunk blocks per pass of the other rows; *x_lds: 1 when each workgroup stages x in
  * LDS.  Any output pointer may be NULL.  Host code only (no launch, no device access when
  * cu_count > 0).  For diagnostics and tests; no reference counterpart. */

@@ -29,8 +29,8 @@
 //     problems 3).  Lane l handles chunks l, l+64, ... of its rows, so a
 //     wavefront-wide dwordx4 streams 1 KiB of a row contiguously.  Large
 //     grouped launches at M = 1 also use flat rows (K = 1024 / 1536: several
-//     short rows per full load, gemv_rows_flat) and deep rows (one long row,
-//     up to four blocks per round trip, gemv_row_deep); both give every row the
+//     short rows per full load, gemv_rows_flat) and deep rows (two long rows,
+//     five blocks per round trip, gemv_rows_deep); both give every row the
 //     bits gemv_rows gives it.
 //   * A pass covers UU (1..4) consecutive 64-chunk blocks; UU is picked per
 //     pass from the chunks left in the row, so a K=5632 row is one pass of
@@ -571,92 +571,77 @@ __device__ __forceinline__ void gemv_rows_flat(const half_t* x, const uint32_t* 
   }
 }
 
-// One pass of gemv_row_deep: UU blocks of one row, every weight and scale load issued first,
-// then per block its x chunk read from LDS, its chunk sum and its product.  Values and order
-// are gemv_pass's for R = 1, M = 1: lane l adds chunk l + 64 u of the pass after chunk
-// l + 64 (u - 1), each as fmaf(s, dot, acc).
-template <int UU>
-__device__ __forceinline__ void gemv_deep_pass(const char* prow, const char* srow, int chunks, int scale_shift,
-                                               int cb, int lane, float& acc, bool first) {
-  u32x4 wv[UU];
-  half_t sv[UU];
-#pragma unroll
-  for (int u = 0; u < UU; ++u) {
-    const uint32_t c = (uint32_t)min(cb + lane + 64 * u, chunks - 1);
-    wv[u] = load_u32x4_stream(prow + 16u * c);
-    sv[u] = *reinterpret_cast<const half_t*>(srow + 2u * (c >> scale_shift));
-  }
-  if (first) {
-    wait_vmcnt<2 * UU>();  // the x copy has landed (only this pass's 2 UU loads follow it)
-    __syncthreads();
-  }
-  __builtin_amdgcn_sched_barrier(0);  // every load of the pass ahead of the math
-#pragma unroll
-  for (int u = 0; u < UU; ++u) {
-    const int c = cb + lane + 64 * u;
-    const int xi = 4 * min(c, chunks - 1);
-    u32x4 xm[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) xm[q] = gemv_x_lds[xi + q];
-    const float xs8 = chunk_xsum(xm) * kMinus8TwoPowMinus24;
-    // Every lane computes (past the row's end on its clamped chunk) and keeps the sum only in
-    // range: a branch here would let a pass end with loads never waited for, and the compiler
-    // would then wait for all loads, the x copy included, before the next pass's first weights.
-    ChunkNibbles nb;
-    split_chunk(wv[u], nb);
-    const float next = fmaf((float)sv[u], chunk_dot(nb, xm, xs8), acc);
-    acc = c < chunks ? next : acc;
-  }
-}
-
-// One pass of gemv_row_deep from chunk cb with as many blocks (up to UMAX) as the row has left;
-// returns the next pass's first chunk.
-template <int UMAX>
-__device__ __forceinline__ int gemv_deep_passes(const char* prow, const char* srow, int chunks, int scale_shift,
-                                                int cb, int lane, float& acc, bool first) {
-  const int left = chunks - cb;  // uniform
-  if (UMAX >= 4 && left > 192) {
-    gemv_deep_pass<(UMAX >= 4 ? 4 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
-    return cb + 256;
-  }
-  if (UMAX >= 3 && left > 128) {
-    gemv_deep_pass<(UMAX >= 3 ? 3 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
-    return cb + 192;
-  }
-  if (UMAX >= 2 && left > 64) {
-    gemv_deep_pass<(UMAX >= 2 ? 2 : 1)>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
-    return cb + 128;
-  }
-  gemv_deep_pass<1>(prow, srow, chunks, scale_shift, cb, lane, acc, first);
-  return cb + 64;
-}
-
-// Deep rows (M = 1, x in LDS): one row per wavefront, up to UMAX 64-chunk blocks per memory
-// round trip.  A pass holds its weights and scales (5 registers per block) and one chunk of
-// x at a time, so three blocks per pass fit the register budget of a full-occupancy launch
-// (gemv_rows keeps every block's x of a pass in registers).  Chunks, products, their order and
-// the one-row reduction are gemv_rows' for R = 1, so the row has the same bits as there.
-template <int UMAX>
-__device__ __forceinline__ void gemv_row_deep(const half_t* x, const uint32_t* packed, const half_t* scales,
-                                              half_t* y, int N, int K, int scale_shift, int row, int lane) {
+// Deep rows (M = 1, x in LDS): rows row0 and row0 + 1, of B = ceil(K / 2048) 64-chunk blocks each,
+// as 2 B (row, block) items - the first row's blocks, then the second's - loaded P at a time,
+// every load of a pass issued before its math.  A pass holds its weights and scales (5
+// registers per item) and one chunk of x at a time.  Each row's chunks are added in gemv_rows'
+// order (lane l: chunks l, l + 64, ..., each as fmaf(s, dot, acc)) and the pair is reduced with
+// its two-row tree, so every row has the bits gemv_rows gives it.  Two rows per wavefront halve
+// the workgroups, and with them the copies of x (17.5 KiB each at K = 8960), against one row
+// per wavefront for the same two round trips (Qwen2.5's 7 linears 6.46-6.51 -> 6.31-6.34 us on
+// MI355X; three rows per wavefront in two or three passes measured slower).
+template <int P>
+__device__ __forceinline__ void gemv_rows_deep(const half_t* x, const uint32_t* packed, const half_t* scales,
+                                               half_t* y, int N, int K, int scale_shift, int row0, int lane) {
   stage_x_lds(x, K >> 3, lane);
   uintptr_t pa = (uintptr_t)packed, sa = (uintptr_t)scales;  // see gemv_rows
   asm volatile("" : "+s"(pa), "+s"(sa));
   const char* pk = (const char*)(const __attribute__((address_space(1))) char*)pa;
   const char* sc = (const char*)(const __attribute__((address_space(1))) char*)sa;
   const int chunks = K >> 5;
-  const size_t n = (size_t)min(row, N - 1);
-  const char* prow = pk + n * (size_t)(K >> 1);
-  const char* srow = sc + n * (size_t)((chunks >> scale_shift) * 2);
-  // The first pass always spans UMAX blocks (blocks past the row's end load its last chunk and
-  // add nothing): one code path from the x copy to the first weights, so the compiler's wait
-  // analysis sees no other pass's loads before them and does not wait for the copy.
-  float acc = 0.0f;
-  gemv_deep_pass<UMAX>(prow, srow, chunks, scale_shift, 0, lane, acc, true);
-  for (int cb = 64 * UMAX; cb < chunks;) cb = gemv_deep_passes<UMAX>(prow, srow, chunks, scale_shift, cb, lane, acc, false);
-  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+  const int nb = (chunks + 63) >> 6;
+  const int items = 2 * nb;
+  const size_t srow_bytes = (size_t)((chunks >> scale_shift) * 2);
+  const size_t na = (size_t)min(row0, N - 1), nr = (size_t)min(row0 + 1, N - 1);  // past N: clamped, not stored
+  const char* prow0 = pk + na * (size_t)(K >> 1);
+  const char* prow1 = pk + nr * (size_t)(K >> 1);
+  const char* srow0 = sc + na * srow_bytes;
+  const char* srow1 = sc + nr * srow_bytes;
+  float acc0 = 0.0f, acc1 = 0.0f;
+  for (int i0 = 0; i0 < items; i0 += P) {  // uniform
+    u32x4 wv[P];
+    half_t sv[P];
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      // Items past the end load the last item again (masked below), so every pass issues P
+      // loads of each kind: the first pass's wait counts on that.
+      const int it = min(i0 + u, items - 1);
+      const bool second = it >= nb;
+      const uint32_t c = (uint32_t)min(64 * (second ? it - nb : it) + lane, chunks - 1);
+      wv[u] = load_u32x4_stream((second ? prow1 : prow0) + 16u * c);
+      sv[u] = *reinterpret_cast<const half_t*>((second ? srow1 : srow0) + 2u * (c >> scale_shift));
+    }
+    if (i0 == 0) {
+      wait_vmcnt<2 * P>();  // the x copy has landed (only this pass's 2 P loads follow it)
+      __syncthreads();
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass ahead of the math
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int it = i0 + u;
+      const bool second = it >= nb;
+      const int c = 64 * (second ? it - nb : it) + lane;
+      const int xi = 4 * min(c, chunks - 1);
+      u32x4 xm[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xm[q] = gemv_x_lds[xi + q];
+      const float xs8 = chunk_xsum(xm) * kMinus8TwoPowMinus24;
+      // Every lane computes (past the row's end on its clamped chunk) and keeps the sum only in
+      // range, with selects: a branch here would let a pass end with loads never waited for, and
+      // the compiler would then wait for all loads, the x copy included, before the next pass's
+      // first weights.
+      ChunkNibbles nbl;
+      split_chunk(wv[u], nbl);
+      const bool in_range = it < items && c < chunks;
+      const float next = fmaf((float)sv[u], chunk_dot(nbl, xm, xs8), second ? acc1 : acc0);
+      acc0 = in_range && !second ? next : acc0;
+      acc1 = in_range && second ? next : acc1;
+    }
+  }
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc0), __float_as_uint(acc1), false, false);
   const float tot = half_sum_lanes31_63(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
-  if (lane == 31 && row < N) y[row] = (half_t)(tot * kTwoPow24);
+  const int n = row0 + (lane >> 5);
+  if ((lane & 31) == 31 && n < N) y[n] = (half_t)(tot * kTwoPow24);
 }
 
 // One problem: every argument is a scalar kernel argument, preloaded into SGPRs, so a
@@ -764,8 +749,9 @@ __global__ __launch_bounds__(64 * kGemvWavesPerBlock) void gemv_grouped_kernel(i
         return;
       }
       if (nkw.w == kGemvDeep) {
-        gemv_row_deep<kGemvDeepBlocks>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y, (const half_t*)(gh_t)ptr.z,
-                         (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift, gwave - nkw.z, lane);
+        gemv_rows_deep<kGemvDeepPass>((const half_t*)(gh_t)ptr.x, (const uint32_t*)(gu_t)ptr.y,
+                                      (const half_t*)(gh_t)ptr.z, (half_t*)(gy_t)ptr.w, nkw.x, nkw.y, scale_shift,
+                                      (gwave - nkw.z) * 2, lane);
         return;
       }
     }
@@ -930,9 +916,9 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   for (int i = 0; i < count; ++i) p.rows[i] = p.rows_per_wave;
   // Large grouped launches (two rows per wavefront) shape each problem's rows:
   //   * M = 1, x in LDS: K = 1024 / 1536 problems take flat rows (full 1 KiB loads), and rows
-  //     longer than one 64-chunk block one row per wavefront with up to kGemvDeepBlocks blocks
-  //     per round trip, if the launch then still fits the wave slots (Qwen2.5's 7 linears at
-  //     M = 1: 6.85 -> 6.39 us on MI355X; TinyLlama's do not fit, and keep their plan).
+  //     longer than one 64-chunk block deep rows (two per wavefront, kGemvDeepPass blocks per
+  //     round trip), if the launch then still fits the wave slots (Qwen2.5's 7 linears at
+  //     M = 1: 6.85 -> 6.31 us on MI355X; TinyLlama's do not fit, and keep their plan).
   //   * A launch whose wavefronts outnumber the wave slots (8 per SIMD) runs its last
   //     wavefronts in a second round, a full memory round trip after the others.  The largest
   //     two-row problems then take three rows per wavefront, just enough of them for the grid

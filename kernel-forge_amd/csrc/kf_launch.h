@@ -62,19 +62,20 @@ inline int gemv_flat_rows(int K) {
   const int c = K / 32, e = 64 - c;
   return (e <= c && c % e == 0 && c / e <= 3) ? c / e + 1 : 0;
 }
-// Deep rows (M = 1, grouped launches with wavefront slots to spare): one long row per wavefront,
-// up to three 64-chunk blocks per memory round trip (gemv_row_deep in kf_gemv.hip).
+// Deep rows (M = 1, grouped launches with wavefront slots to spare): two long rows per
+// wavefront, their 64-chunk blocks loaded kGemvDeepPass at a time per memory round trip
+// (gemv_rows_deep in kf_gemv.hip).
 constexpr int kGemvDeep = 8;
 // GemvPlan::rows_per_wave of a grouped launch (M = 1, x in LDS) with flat or deep rows among its
 // problems.  Its kernel is an instantiation of its own, so launches without such rows keep the
-// mixed kernel's code and registers.  kGemvDeepBlocks: 64-chunk blocks per pass of a deep row,
-// as many as keep the kernel at 8 wavefronts per SIMD (kernelforge/build.py checks it; five
-// blocks cost one wavefront per SIMD and measured no faster on Qwen2.5's 7 linears).
+// mixed kernel's code and registers.  kGemvDeepPass: (row, block) loads per pass of a deep
+// wavefront, as many as keep the kernel at 8 wavefronts per SIMD (kernelforge/build.py checks
+// it): a K = 8960 row pair is two passes of five.
 constexpr int kGemvRowsShaped = 4;
-constexpr int kGemvDeepBlocks = 4;
+constexpr int kGemvDeepPass = 5;
 // Rows one wavefront owns for a GemvPlan::rows / GemvSlot::rows entry.
 inline int gemv_entry_rows(int entry) {
-  return entry == kGemvDeep ? 1 : (entry > kGemvFlat ? entry - kGemvFlat : entry);
+  return entry == kGemvDeep ? 2 : (entry > kGemvFlat ? entry - kGemvFlat : entry);
 }
 
 struct GemvPlan {

@@ -148,7 +148,7 @@ SLOTS = 32 * CUS  # 8 wavefronts per SIMD, 4 SIMDs per CU
 
 
 def _entry_rows(entry: int) -> int:
-    return 1 if entry == _lib.KF_GEMV_DEEP else (entry - _lib.KF_GEMV_FLAT if entry > _lib.KF_GEMV_FLAT else entry)
+    return 2 if entry == _lib.KF_GEMV_DEEP else (entry - _lib.KF_GEMV_FLAT if entry > _lib.KF_GEMV_FLAT else entry)
 
 
 def _waves(shapes, rows, x_lds) -> int:
@@ -173,9 +173,10 @@ def test_gemv_plan_benchmarked_sets_without_gpu():
     qwen = _lib.gemv_plan(1, QWEN_SEVEN, CUS)
     assert qwen["kernel"] == _lib.KF_GEMV_KERNEL_SHAPED and qwen["x_lds"] and qwen["unroll"] == 1
     assert qwen["rows"] == [flat4] * 6 + [_lib.KF_GEMV_DEEP]  # K = 1536: 4 rows in 3 full loads; down: deep
-    assert _waves(QWEN_SEVEN, qwen["rows"], True) == 6912 <= SLOTS
+    assert _waves(QWEN_SEVEN, qwen["rows"], True) == 6144 <= SLOTS
     tl = _lib.gemv_plan(1, TL_SEVEN, CUS)
-    # deep rows for down would need 9,984 wavefronts: the plan keeps two rows and gives gate three
+    # deep rows (two per wavefront, like plain rows) leave 8,960 wavefronts for 8,192 slots: the
+    # plan keeps plain two-row down and gives gate three rows
     assert tl["kernel"] == _lib.KF_GEMV_KERNEL_MIXED and tl["rows"] == [2, 2, 2, 2, 3, 2, 2]
     assert _waves(TL_SEVEN, tl["rows"], True) == 8024 <= SLOTS
 

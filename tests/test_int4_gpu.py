@@ -475,10 +475,11 @@ def test_grouped_guard_bands_three_row_waves(m, k):
 @pytest.mark.parametrize("group", [64, 128])
 def test_grouped_flat_and_deep_rows(group):
     """The shaped grouped launch (M = 1): flat rows for K = 1536 (four rows in three full loads) and
-    K = 1024 (two rows in one), with N leaving the last wavefront part empty, and deep rows for
-    K = 8960 (a four-block pass, then 24 chunks), 6144 (one three-block pass) and 2304 (one
-    two-block pass of 72 chunks), beside a plain two-row problem: outputs inside their guard
-    bands, bit-identical to single launches, within tolerance of the oracle."""
+    K = 1024 (two rows in one), with N leaving the last wavefront part empty, and deep rows (two
+    per wavefront, five (row, block) loads per pass) for K = 8960 (two passes of five), 6144 (a
+    pass of five, then one) and 2304 (one pass, one clamped load), odd N leaving a wavefront's
+    second row past the end, beside a plain two-row problem: outputs inside their guard bands,
+    bit-identical to single launches, within tolerance of the oracle."""
     shapes = [(1534, 1536), (1023, 1024), (3001, 1536), (701, 8960), (515, 2304), (257, 2048), (6, 1536),
               (130, 6144)]
     plan = _lib.gemv_plan(1, shapes)
