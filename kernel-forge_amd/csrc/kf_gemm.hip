@@ -914,7 +914,7 @@ constexpr int kMaxSplits = 12;  // the largest split count the fit was measured 
 GemmPlan plan_for(int K, int tile, int splits) {
   GemmPlan p;
   p.skinny = false;
-  p.sk = SkinnyPlan{0, 0, 0, false, 0};
+  p.sk = SkinnyPlan{0, 0, 0, false, 0, 1};
   p.tile = tile;
   p.block_m = kTiles[tile].bm;
   p.block_n = kTiles[tile].bn;
@@ -946,9 +946,11 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
 // Kernel choice.
 //   * The skinny kernel (one weight stream, K split inside the workgroup) for M <= 8, for
 //     M <= 16 when K <= 4096, and up to M = 32 for small matrices (N*K <= 4.2M: TinyLlama q/o
-//     and k/v).  The rule depends on N only through that last clause, so concatenated q|k|v or
-//     gate|up rows take the same kernel as the separate layers for M <= 16 (bit-identical
-//     columns).
+//     and k/v) or grids of at most one workgroup per CU (TinyLlama gate/up, whose workgroups
+//     take two column blocks, M = 20..32: 7.3 -> 6.0-7.0 us; q|k|v fused 7.1 -> 5.1-6.0 us; Qwen2.5
+//     gate/up at 560 workgroups and TinyLlama gate|up fused at 704 stay faster tiled).  The rule
+//     depends on N only through those last two clauses, so concatenated q|k|v or gate|up rows
+//     take the same kernel as the separate layers for M <= 16 (bit-identical columns).
 //   * Otherwise the tile and split-K factor that minimise a fitted cost: each XCD runs its
 //     share of the tiles x splits workgroups in rounds of blocks_per_cu * cu_count / 8; a round
 //     costs the tile entry's us_per_gmac * 1e-9 * BM * BN * (K / splits) + us_fixed, and
@@ -958,7 +960,8 @@ GemmPlan gemm_plan_with_tile(int M, int N, int K, int cu_count, int tile) {
 GemmPlan gemm_plan(int M, int N, int K, int cu_count) {
   const int cus = cu_count > 0 ? cu_count : 256;
   const bool k128 = K % 128 == 0;
-  if (M <= kSkinnyMaxM && k128 && (M <= 8 || (K <= 4096 && (M <= 16 || (long)N * K <= 4200000L)))) {
+  const bool one_round = (long)ceil_div(N, 16 * skinny_col_blocks(N, cus)) <= cus;
+  if (M <= kSkinnyMaxM && k128 && (M <= 8 || (K <= 4096 && (M <= 16 || (long)N * K <= 4200000L || one_round)))) {
     GemmPlan p = plan_for(K, kTile64, 1);
     p.skinny = true;
     p.sk = skinny_plan(M, N, K, cu_count);

@@ -135,14 +135,17 @@ hipError_t gemv_qkv_rope_launch(const GemvProblem& problem, const GemvFused& f, 
 // gemm_plan (kf_gemm.hip) picks it for small M by the measured rule stated there.
 constexpr int kSkinnyMaxM = 32;
 struct SkinnyPlan {
-  int m_tiles;   // 16-row tiles of M (1..2)
-  int ks_waves;  // wavefronts per workgroup, each a contiguous run of 128-k super-steps
-  int unroll;    // super-steps whose weight loads are in flight together
-  bool x_lds;    // x fragments from each wavefront's LDS copy of its k range (else from L2)
-  int lds_bytes; // dynamic LDS per workgroup
+  int m_tiles;    // 16-row tiles of M (1..2)
+  int ks_waves;   // wavefronts per workgroup, each a contiguous run of 128-k super-steps
+  int unroll;     // super-steps whose weight loads are in flight together
+  bool x_lds;     // x fragments from each wavefront's LDS copy of its k range (else from L2)
+  int lds_bytes;  // dynamic LDS per workgroup
+  int col_blocks; // 16-column blocks per workgroup (1..2)
 };
 constexpr int kSkinnyMaxLds = 160 * 1024;  // LDS of a gfx950 CU
 SkinnyPlan skinny_plan(int M, int N, int K, int cu_count);
+// 16-column blocks per skinny workgroup for N on cu_count CUs (SkinnyPlan::col_blocks).
+int skinny_col_blocks(int N, int cu_count);
 hipError_t skinny_launch(const SkinnyPlan& p, const void* x, const void* packed, const void* scales, void* y, int M,
                          int N, int K, int group_size, bool blocked, hipStream_t stream);
 // MFMA-16 block copy of packed / scales (kf_skinny.hip): sizes in int32 words and fp16 scales.

@@ -57,8 +57,10 @@ def test_reorder_matches_oracle(n, k, g):
     assert np.array_equal(sr.cpu().numpy().view(np.uint16), want_s.view(np.uint16))
 
 
+# gate, wide_a and wide_b take two 16-column blocks per skinny workgroup on 256 CUs
+# (SkinnyPlan::col_blocks; N is a multiple of 64 on the GEMM path, so those workgroups are whole).
 LAYERS = {"qo": (2048, 2048), "kv": (256, 2048), "gate": (5632, 2048), "down": (2048, 5632),
-          "qwen_down": (1536, 8960), "ragged": (320, 1152)}
+          "qwen_down": (1536, 8960), "ragged": (320, 1152), "wide_a": (4160, 2048), "wide_b": (6016, 1024)}
 
 
 @pytest.mark.parametrize("layer", list(LAYERS))
