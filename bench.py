@@ -50,6 +50,9 @@ Protocol
   TFLOPS = 2*M*N*K / time, for gate and the 7-layer sum, each beside
   hipBLASLt's dense fp16 GEMM on the same shape (torch F.linear with fp16
   weights, same protocol).
+* per-layer, step-structure, Qwen2.5 (config 3) and quantize legs: graph replays
+  of several steps, the median of five timed regions, each after an untimed
+  run of the same graph.
 * cpu_baseline: the reference's FP32 dequant + matmul restated in torch
   (oracle/cpu_baseline.py) on the host cores over a bounded sample, per call
   and matmul-only.
@@ -814,7 +817,7 @@ def main() -> int:
         structures = {}
         for label, fn, launches in (("decoder_4_launches", step_decoder, 4), ("separate_7_launches", step_separate, 7)):
             gs = GraphSteps(torch, fn, copies)
-            ms = gs.event_avg_ms(8 * copies)
+            ms = statistics.median(gs.event_avg_ms(8 * copies) for _ in range(5))
             structures[label] = {"launches": launches, "us_per_step": round(ms * 1e3, 3),
                                  "gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
                                  "pct_of_copy": round(100 * step_bytes / (ms * 1e-3) / 1e9 / ceil["hbm_copy_gbps"], 1)}
@@ -823,7 +826,7 @@ def main() -> int:
         for nm in names:
             i = idx[nm]
             gs = GraphSteps(torch, lambda r, nm=nm: single(r, nm), copies)
-            ms = gs.event_avg_ms(8 * copies)
+            ms = statistics.median(gs.event_avg_ms(8 * copies) for _ in range(5))
             b = algo_bytes(1, layers[i]["N"], layers[i]["K"])
             per_layer[nm] = {"N": layers[i]["N"], "K": layers[i]["K"], "bytes": b, "us": round(ms * 1e3, 3),
                              "gbps": round(b / (ms * 1e-3) / 1e9, 1),
@@ -838,7 +841,7 @@ def main() -> int:
         q_xs = [ly["x"].cuda() for ly in qlayers]
         gs = GraphSteps(torch, lambda r: ops.int4_linear_grouped(q_xs, [p for p, _ in q_dev[r]],
                                                                  [s for _, s in q_dev[r]], GROUP), q_copies)
-        q_ms = gs.event_avg_ms(8 * q_copies)
+        q_ms = statistics.median(gs.event_avg_ms(8 * q_copies) for _ in range(5))
         q_gbps = q_bytes / (q_ms * 1e-3) / 1e9
         qwen = {"workload": "qwen2.5_1.5b_7_linears_m1_g128", "shapes_NxK": [[n, k] for _, n, k in QWEN_LAYERS],
                 "bytes_per_step": q_bytes, "us_per_step": round(q_ms * 1e3, 3), "gbps": round(q_gbps, 1),
@@ -893,7 +896,7 @@ def main() -> int:
         qcopies = max(2, -(-(2 * MALL_BYTES) // in_bytes))
         wq = [torch.randn(qn, qk, device="cuda") * 0.02 for _ in range(qcopies)]
         gs = GraphSteps(torch, lambda r: ops.int4_quantize(wq[r], GROUP), qcopies)
-        ms = gs.event_avg_ms(4 * qcopies)
+        ms = statistics.median(gs.event_avg_ms(4 * qcopies) for _ in range(5))
         gbps = (in_bytes + out_bytes) / (ms * 1e-3) / 1e9
         w_host = wq[0].cpu()
         kq.quantize_weight(w_host, GROUP)
