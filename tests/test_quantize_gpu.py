@@ -91,6 +91,41 @@ def test_quantize_divides_like_the_cpu():
     assert torch.equal(gpu.packed.cpu(), cpu.packed) and torch.equal(gpu.scales.cpu(), cpu.scales)
 
 
+@pytest.mark.parametrize("group", [64, 128])
+def test_quantize_near_half_integers(group):
+    """Values within a few ulps of (j + 1/2) * s, for 300 scales s: the kernel's reciprocal
+    product must fall back to the division wherever the two could round apart, including the
+    values for which fl32(v / s) is exactly j + 1/2 although v / s is not (ties by double
+    rounding, resolved to even)."""
+    rng = np.random.default_rng(5)
+    scales = np.unique(np.concatenate([
+        (2.0 ** rng.uniform(-13, 9, 280)).astype(np.float16),  # normal fp16 scales
+        np.float16([2**-14, 1.0, 0.5, 0.75, 1.5, 3.0, 65504 / 7 / 2]),
+    ]).astype(np.float32))
+    combos = [(j, n) for j in range(-7, 7) for n in range(-3, 4)]
+    rows = []
+    for s in scales:
+        row = np.empty(256, np.float32)
+        for g0 in range(0, 256, group):
+            row[g0] = np.float32(7.0) * s  # absmax 7 s: the group's scale is s exactly
+            for slot in range(1, group):
+                j, n = combos[(g0 + slot) % len(combos)]
+                v = np.float32((j + 0.5) * s)  # exact: 4 + 11 significant bits
+                for _ in range(abs(n)):
+                    v = np.nextafter(v, np.float32(np.inf) if n > 0 else np.float32(-np.inf), dtype=np.float32)
+                row[g0 + slot] = v
+        rows.append(row)
+    w = np.stack(rows)
+    # The crafted set holds double-rounding ties: v != (j + 1/2) s, yet fl32(v / s) = j + 1/2.
+    q = w / np.repeat(scales[:, None], 256, axis=1)
+    half = np.abs(q - np.floor(q)) == np.float32(0.5)
+    exact_half = np.zeros_like(half)
+    for i, s in enumerate(scales):
+        exact_half[i] = (np.floor(q[i]) + 0.5).astype(np.float32) * s == w[i]
+    assert (half & ~exact_half).sum() > 100, "no double-rounding ties in the crafted values"
+    _assert_matches_oracle(torch.from_numpy(w), group)
+
+
 def test_quantize_noncontiguous_and_offset_inputs():
     base = torch.randn(64, 520, device=DEV) * 0.02
     view = base[:, 4:516]  # non-contiguous, storage offset of 16 bytes
