@@ -934,8 +934,15 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   p.unroll = waves >= 12 * cus ? 1 : (blocks < u_max ? blocks : u_max);
   // Per-lane x loads move 64 bytes of x through the texture path for every 16 bytes of a
   // row; one LDS copy per workgroup removes that traffic (7 TinyLlama linears at M = 1:
-  // 6.9 -> 6.3 us on MI355X) wherever x fits the LDS budget.
-  p.x_lds = x_lds_bytes(M, max_k) <= (size_t)kGemvMaxLdsX;
+  // 6.9 -> 6.3 us on MI355X) wherever x fits the LDS budget.  The budget is what leaves every
+  // workgroup of the launch resident: 20 KiB for launches of eight or more workgroups per CU,
+  // the CU's 160 KiB shared among fewer.  The larger copies take M = 2-8 rows of long x into
+  // LDS in single-problem launches (same bits; MI355X, TinyLlama down M = 2 / 3 / 4:
+  // 5.24 / 6.41 / 7.64 -> 3.86 / 5.26 / 6.11 us, Qwen2.5 down 7.66 / 9.37 / 11.58 -> 5.67 /
+  // 7.20 / 8.54 us, q/o and gate at M = 8 -25%).
+  const long wgs_per_cu = ((waves + kGemvWavesPerBlock - 1) / kGemvWavesPerBlock + cus - 1) / cus;
+  const long budget = std::max<long>(kGemvMaxLdsX, kLdsPerCu / wgs_per_cu / 1024 * 1024);
+  p.x_lds = x_lds_bytes(M, max_k) <= (size_t)budget;
   for (int i = 0; i < count; ++i) p.rows[i] = p.rows_per_wave;
   // Large grouped launches (two rows per wavefront) shape each problem's rows:
   //   * M = 1, x in LDS: K = 1024 / 1536 problems take flat rows (full 1 KiB loads), and rows
@@ -1006,7 +1013,12 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
     const GemvProblem& q = problems[0];
     const int blocks = xcd_grid(ceil_div(ceil_div(q.N, plan.rows_per_wave), kGemvWavesPerBlock));
     const size_t lds = plan.x_lds ? x_lds_bytes(M, q.K) : 0;
-    hipLaunchKernelGGL(reinterpret_cast<GemvFn>(pick<false>(M, plan)), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
+    void* fn = pick<false>(M, plan);
+    if (lds > 65536) {  // dynamic LDS beyond 64 KiB is opted into per kernel
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPerCu);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(reinterpret_cast<GemvFn>(fn), dim3(blocks), dim3(64 * kGemvWavesPerBlock),
                        lds, stream, static_cast<const half_t*>(q.x), static_cast<const uint32_t*>(q.packed),
                        static_cast<const half_t*>(q.scales), static_cast<half_t*>(q.y), q.N, q.K, shift);
     return hipGetLastError();
@@ -1040,7 +1052,12 @@ hipError_t gemv_launch(const GemvPlan& plan, const GemvProblem* problems, int co
   }
   const int blocks = xcd_grid(ceil_div(waves, kGemvWavesPerBlock));
   const size_t lds = plan.x_lds ? x_lds_bytes(M, max_k) : 0;
-  hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(pick<true>(M, plan)), dim3(blocks),
+  void* fn = pick<true>(M, plan);
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPerCu);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(reinterpret_cast<GemvGroupedFn>(fn), dim3(blocks),
                      dim3(64 * kGemvWavesPerBlock), lds, stream, count, shift, bounds[0], bounds[1], bounds[2],
                      bounds[3], bounds[4], bounds[5], bounds[6], bounds[7], table);
   return hipGetLastError();

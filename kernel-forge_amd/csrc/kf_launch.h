@@ -47,6 +47,9 @@ constexpr int kGemvWavesPerBlock = 4;  // 256-thread workgroups
 // Largest x (M * K fp16 values, in bytes) a workgroup copies into LDS; 20 KiB keeps eight
 // workgroups (32 wavefronts) per CU within the 160 KiB of LDS.
 constexpr int kGemvMaxLdsX = 20480;
+// A launch with fewer workgroups per CU gives each a larger copy: the CU's 160 KiB over the
+// workgroups it holds (beyond 64 KiB the launch opts into the larger dynamic LDS).
+constexpr int kLdsPerCu = 160 * 1024;
 
 // GemvPlan::rows_per_wave of a grouped launch whose problems take 2 or 3 rows per wavefront
 // each (GemvPlan::rows, GemvSlot::rows); also the grouped kernel's template rows for it.

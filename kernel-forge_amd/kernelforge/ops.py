@@ -24,7 +24,7 @@ from kernelforge import _lib
 # largest M at which the sum of GEMV times over the layer shapes beats the GEMM's
 # (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
 # skinny MFMA kernel for small M, then the tiled MFMA kernels.
-GEMV_MAX_M = 3
+GEMV_MAX_M = 4
 # The reference's int4_matmul sends M <= 7 to its GEMV, which accepts every N, and M >= 8
 # to its GEMM, which rejects N % 64 != 0 (kernelforge/ops.py:193,204-214).  Our MFMA kernels
 # need N % 64 == 0 as well, so between GEMV_MAX_M and 7 a shape the GEMM cannot take stays
