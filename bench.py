@@ -106,7 +106,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-m2048", action="store_true", help="skip the M=2048 GEMM leg")
-    ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "blas_m2048", "copy", "decode"],
+    ap.add_argument("--profile", choices=["gemv_grouped", "gemm_m2048", "blas_m2048", "copy", "decode", "quantize"],
                     help="only launch one kernel --profile-iters times (for rocprofv3 --pmc runs) and exit")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
@@ -168,6 +168,8 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
       kernel that calibrates FETCH_SIZE / WRITE_SIZE.
     decode:      the INT4 TinyLlama of the e2e leg: 16-token prompt, capture, --profile-iters graph
       replays of the decode step (for a kernel trace of one token).
+    quantize:    the on-device quantize + pack of the quantize leg (fp32 gate 5632 x 2048, G=128),
+      weights rotated over more than twice the MALL as in that leg.
     """
     stream = torch.cuda.current_stream().cuda_stream
     if args.profile == "copy":
@@ -193,6 +195,12 @@ def profile_only(args, torch, lib, kl, ops, kq) -> int:
         x = torch.randn(2048, gate["K"], dtype=torch.float16, device="cuda")
         for _ in range(args.profile_iters):
             ops.int4_gemm(x, p, s, GROUP)
+    elif args.profile == "quantize":
+        qn, qk = 5632, 2048
+        qcopies = max(2, -(-(2 * MALL_BYTES) // (qn * qk * 4)))
+        wq = [torch.randn(qn, qk, device="cuda") * 0.02 for _ in range(qcopies)]
+        for i in range(args.profile_iters):
+            ops.int4_quantize(wq[i % qcopies], GROUP)
     elif args.profile == "blas_m2048":
         x = torch.randn(2048, 2048, dtype=torch.float16, device="cuda")
         w = torch.randn(5632, 2048, dtype=torch.float16, device="cuda")
