@@ -942,7 +942,8 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
   // 7.20 / 8.54 us, q/o and gate at M = 8 -25%).
   const long wgs_per_cu = ((waves + kGemvWavesPerBlock - 1) / kGemvWavesPerBlock + cus - 1) / cus;
   const long budget = std::max<long>(kGemvMaxLdsX, kLdsPerCu / wgs_per_cu / 1024 * 1024);
-  p.x_lds = x_lds_bytes(M, max_k) <= (size_t)budget;
+  const size_t xb = x_lds_bytes(M, max_k);
+  p.x_lds = xb <= (size_t)budget;
   for (int i = 0; i < count; ++i) p.rows[i] = p.rows_per_wave;
   // Large grouped launches (two rows per wavefront) shape each problem's rows:
   //   * M = 1, x in LDS: K = 1024 / 1536 problems take flat rows (full 1 KiB loads), and rows
@@ -981,7 +982,23 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
           if (p.rows[i] == kGemvDeep) p.rows[i] = 2;
       }
     }
-    const long slots = 32L * cus;
+    long slots = 32L * cus;
+    if (!p.x_lds && M == 2 && xb <= (size_t)kLdsPerCu / 2) {
+      // x past the default budget (M = 2 with K > 5120): in LDS after all when the launch, with
+      // three rows per wavefront for every two-row problem, fits the workgroups the LDS holds;
+      // the shaping below then aims at that many wave slots (TinyLlama's 7 linears: 22 KiB of x,
+      // seven workgroups per CU).
+      const long lds_slots = (long)(kLdsPerCu / xb) * kGemvWavesPerBlock * cus;
+      long w3 = 0;
+      for (int i = 0; i < count; ++i) {
+        const long r = p.rows[i] == 2 ? 3 : gemv_entry_rows(p.rows[i]);
+        w3 += ((N[i] + r - 1) / r + kGemvWavesPerBlock - 1) / kGemvWavesPerBlock * kGemvWavesPerBlock;
+      }
+      if (w3 <= lds_slots) {
+        p.x_lds = true;
+        slots = lds_slots;
+      }
+    }
     long total = total_waves();
     bool three = false;
     while (total > slots) {  // two-row problems (plain or flat) to three rows, largest first

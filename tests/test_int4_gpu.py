@@ -152,6 +152,32 @@ def test_grouped_gemv_bit_identical_to_single(error_log, m, group):
         assert err <= REL_TOL, f"{name}: {err:.3e}"
 
 
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_tinyllama_m2_x_in_lds(error_log, group):
+    """The 7 TinyLlama linears at M = 2 in one launch: x of down (22 KiB) exceeds the default LDS
+    budget, yet the plan stages x in LDS, with three rows per wavefront for the largest problems so
+    the launch fits the workgroups the LDS holds; every output bit-identical to its single launch
+    and within tolerance of the oracle."""
+    plan = _lib.gemv_plan(2, [LAYER_SHAPES[n] for n in TL_SEVEN])
+    assert plan["x_lds"] and 3 in plan["rows"], plan
+    xs, ps, ss, refs = [], [], [], []
+    for i, name in enumerate(TL_SEVEN):
+        n, k = LAYER_SHAPES[name]
+        packed, scales, dp, ds = _weights(n, k, group)
+        x = _x(2, k, 2000 + i)
+        xs.append(torch.from_numpy(x).to(DEV))
+        ps.append(dp)
+        ss.append(ds)
+        refs.append(o.linear_ref_fp32(x, packed, scales, group))
+    ys = ops.int4_gemv_grouped(xs, ps, ss, group)
+    for i, name in enumerate(TL_SEVEN):
+        assert torch.equal(ys[i], ops.int4_gemv(xs[i], ps[i], ss[i], group)), f"{name}: grouped differs from single"
+        err = o.max_rel_err(ys[i].float().cpu().numpy(), refs[i])
+        error_log.add("int4_gemv_grouped", case=name, shape=[2, *LAYER_SHAPES[name]], group=group,
+                      max_rel_err=err, passed=err <= REL_TOL)
+        assert err <= REL_TOL, f"{name}: {err:.3e}"
+
+
 QWEN_SEVEN = [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 1536),
               ("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960)]
 
