@@ -603,13 +603,13 @@ def measure_mfma_peak(torch) -> float:
     return best
 
 
-def make_layers(torch, kq, shapes=TL_LAYERS, seed=1000):
+def make_layers(torch, kq, shapes=TL_LAYERS, seed=1000, group=GROUP):
     """Seeded fp32 weights quantized by the package (the format producer), plus x per layer."""
     layers = []
     for i, (name, n, k) in enumerate(shapes):
         g = torch.Generator().manual_seed(seed + i)
         w = torch.randn(n, k, generator=g) * 0.02
-        qw = kq.quantize_weight(w, GROUP)
+        qw = kq.quantize_weight(w, group)
         x = torch.randn(1, k, generator=g).half()
         layers.append({"name": name, "N": n, "K": k, "packed": qw.packed, "scales": qw.scales, "x": x})
     return layers

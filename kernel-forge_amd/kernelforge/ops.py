@@ -15,8 +15,10 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+from typing import Optional
 
 import torch
+from torch._subclasses.fake_tensor import FakeTensor
 
 from kernelforge import _lib
 
@@ -44,6 +46,19 @@ def _stream_ptr(device: torch.device) -> int:
 
 def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
+
+
+_PLAIN = (torch.Tensor, torch.nn.Parameter)
+
+
+def _traced(tensors) -> bool:
+    """True when a tracer must see the registered op instead of a kernel launch: torch is
+    compiling, a TorchDispatchMode is active (FakeTensorMode, make_fx's proxy mode, ...), or an
+    input is a tensor subclass (a FakeTensor made outside its mode, a functional tensor, ...).
+    Eager calls on plain tensors return False and skip the op dispatcher."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return True
+    return any(t is not None and type(t) not in _PLAIN for t in tensors)
 
 
 def _on(device: torch.device):
@@ -75,7 +90,8 @@ def _check_native(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, g
     Valid inputs pass one combined test (a few microseconds less host time per problem); anything
     else goes through the checks one by one, which raise in the reference's order."""
     dev = x.get_device()
-    if (x.is_cuda and packed.is_cuda and scales.is_cuda and x.is_contiguous() and packed.is_contiguous()
+    if (type(x) in _PLAIN and type(packed) in _PLAIN and type(scales) in _PLAIN
+            and x.is_cuda and packed.is_cuda and scales.is_cuda and x.is_contiguous() and packed.is_contiguous()
             and scales.is_contiguous() and packed.get_device() == dev and scales.get_device() == dev
             and packed.dim() == 2 and scales.dim() == 2 and (group_size == 64 or group_size == 128)
             and scales.shape[0] == packed.shape[0] and scales.shape[1] == x.shape[1] // group_size
@@ -87,6 +103,9 @@ def _check_native(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, g
 def _check_native_each(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> None:
     """_check_native's conditions one at a time, raising the first that fails."""
     for name, t in (("x", x), ("packed", packed), ("scales", scales)):
+        if isinstance(t, FakeTensor) or t.is_meta:
+            raise RuntimeError(f"{name} has no device memory (a fake or meta tensor): trace through int4_linear / "
+                               "kernelforge::int4_matmul, whose fake impl gives the output shape")
         if not t.is_cuda:
             raise RuntimeError(f"{name} must be a CUDA tensor")
         if not t.is_contiguous():
@@ -423,7 +442,7 @@ def int4_linear_grouped(xs: list[torch.Tensor], packed: list[torch.Tensor], scal
         flat.append(x2 if x2.is_contiguous() else x2.contiguous())
     for x2, p, s in zip(flat, packed, scales):
         _check_int4(x2, p, s, group_size)
-    if torch.compiler.is_compiling():
+    if _traced([*flat, *packed, *scales]):
         ys = _int4_matmul_grouped_op(flat, list(packed), list(scales), int(group_size))
     else:  # eager: the op's implementation without the dispatcher (as in int4_linear), checked once
         ys = _matmul_grouped(flat, list(packed), list(scales), int(group_size), checked=True)
@@ -448,9 +467,11 @@ def int4_linear(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, gro
     if not x2.is_contiguous():
         x2 = x2.contiguous()
     _check_int4(x2, packed, scales, group_size)
-    # The registered op kernelforge::int4_matmul whenever torch is compiling or tracing; eager
-    # calls go straight to its implementation (same result), skipping ~14 us of op dispatch.
-    if torch.compiler.is_compiling():
+    # The registered op kernelforge::int4_matmul whenever torch compiles or any tracer or dispatch
+    # mode is looking (torch.compile, FakeTensorMode, make_fx, ...), as the reference always calls
+    # it; eager calls on plain tensors go straight to its implementation (same result), skipping
+    # ~14 us of op dispatch.
+    if _traced((x2, packed, scales)):
         y = _int4_matmul_op(x2, packed, scales, int(group_size))
     else:
         y = _matmul_checked(x2, packed, scales, int(group_size))
@@ -491,30 +512,62 @@ def int4_linear_fused(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tenso
         raise ValueError(f"up must have the shape of x, {tuple(x.shape)}, got {tuple(up.shape)}")
     if norm_weight is not None and norm_weight.shape != (k,):
         raise ValueError(f"norm_weight must be [{k}], got {tuple(norm_weight.shape)}")
-    fused = (m == 1 and k <= _lib.KF_GEMV_FUSED_MAX_K and x.is_cuda and x2.is_contiguous()
-             and x2.data_ptr() % 16 == 0 and (aux is None or (aux.is_contiguous() and aux.data_ptr() % 16 == 0))
-             and (res2 is None or res2.is_contiguous()))
-    if not fused:
-        if norm_weight is not None:
-            x2 = torch.nn.functional.rms_norm(x2, (k,), norm_weight, eps)
-        elif up is not None:
-            x2 = torch.nn.functional.silu(x2) * up.reshape(-1, k)
-        y = int4_linear(x2, packed, scales, group_size)
-        if res2 is not None:
-            y = res2 + y
-        return y.reshape(*lead, n)
-    _check_int4(x2, packed, scales, group_size)
-    _check_native(x2, packed, scales, group_size)
     prologue = (_lib.KF_PROLOGUE_RMSNORM if norm_weight is not None
                 else _lib.KF_PROLOGUE_SWIGLU if up is not None else _lib.KF_PROLOGUE_NONE)
-    lib = _lib.load()
-    y = torch.empty(1, n, dtype=torch.float16, device=x.device)
-    with _on(x.device):
-        status = lib.kf_int4_gemv_fused(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), 1, n, k, int(group_size),
-                                        prologue, _ptr(aux) if aux is not None else None, float(eps),
-                                        _ptr(res2) if res2 is not None else None, _stream_ptr(x.device))
-    _lib.check(status, "int4_gemv_fused")
+    fused = (m == 1 and k <= _lib.KF_GEMV_FUSED_MAX_K and x.is_cuda and x2.is_contiguous()
+             and (aux is None or aux.is_contiguous()) and (res2 is None or res2.is_contiguous()))
+    if not fused:
+        return _fused_composition(x2, packed, scales, group_size, prologue, aux, eps, res2).reshape(*lead, n)
+    _check_int4(x2, packed, scales, group_size)
+    if _traced((x2, packed, scales, aux, res2)):
+        y = _int4_linear_fused_op(x2, packed, scales, int(group_size), prologue, aux, float(eps), res2)
+    else:
+        y = _launch_fused(x2, packed, scales, int(group_size), prologue, aux, float(eps), res2)
     return y.reshape(*lead, n)
+
+
+def _fused_composition(x2: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int, prologue: int,
+                       aux: torch.Tensor | None, eps: float, res2: torch.Tensor | None) -> torch.Tensor:
+    """int4_linear_fused's steps as separate torch ops around int4_linear (shapes the fused launch
+    does not take); x2 [M, K] -> y [M, N]."""
+    k = x2.shape[1]
+    if prologue == _lib.KF_PROLOGUE_RMSNORM:
+        x2 = torch.nn.functional.rms_norm(x2, (k,), aux, eps)
+    elif prologue == _lib.KF_PROLOGUE_SWIGLU:
+        x2 = torch.nn.functional.silu(x2) * aux.reshape(-1, k)
+    y = int4_linear(x2, packed, scales, group_size)
+    return y if res2 is None else res2 + y
+
+
+def _launch_fused(x2: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int, prologue: int,
+                  aux: torch.Tensor | None, eps: float, res2: torch.Tensor | None) -> torch.Tensor:
+    """kf_int4_gemv_fused on int4_linear_fused's validated one-row inputs; y [1, N].  x or the
+    prologue operand off a 16-byte boundary (the launch's LDS copies need it) takes the
+    composition instead, with the same result."""
+    if x2.data_ptr() % 16 or (aux is not None and aux.data_ptr() % 16):
+        return _fused_composition(x2, packed, scales, group_size, prologue, aux, eps, res2)
+    _check_native(x2, packed, scales, group_size)
+    lib = _lib.load()
+    n, k = packed.shape[0], x2.shape[1]
+    y = torch.empty(1, n, dtype=torch.float16, device=x2.device)
+    with _on(x2.device):
+        status = lib.kf_int4_gemv_fused(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), 1, n, k, group_size,
+                                        prologue, _ptr(aux) if aux is not None else None, eps,
+                                        _ptr(res2) if res2 is not None else None, _stream_ptr(x2.device))
+    _lib.check(status, "int4_gemv_fused")
+    return y
+
+
+@torch.library.custom_op("kernelforge::int4_linear_fused", mutates_args=())
+def _int4_linear_fused_op(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int,
+                          prologue: int, aux: Optional[torch.Tensor], eps: float,
+                          residual: Optional[torch.Tensor]) -> torch.Tensor:
+    return _launch_fused(x, packed, scales, group_size, prologue, aux, eps, residual)
+
+
+@_int4_linear_fused_op.register_fake
+def _(x, packed, scales, group_size, prologue, aux, eps, residual):
+    return x.new_empty(1, packed.shape[0])
 
 
 def int4_qkv_rope_cache(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int, *,
@@ -548,19 +601,50 @@ def int4_qkv_rope_cache(x: torch.Tensor, packed: torch.Tensor, scales: torch.Ten
     if pos.dtype != torch.int64 or pos.numel() != 1 or pos.device != x.device:
         raise ValueError("pos must be one int64 on the device of x")
     if norm_weight is not None and (norm_weight.dtype != torch.float16 or norm_weight.shape != (k,)
-                                    or not norm_weight.is_contiguous() or norm_weight.data_ptr() % 16):
+                                    or not norm_weight.is_contiguous()):
         raise ValueError(f"norm_weight must be a contiguous, 16-byte aligned fp16 [{k}]")
     x2 = x2.contiguous()
     _check_int4(x2, packed, scales, group_size)
-    _check_native(x2, packed, scales, group_size)
-    lib = _lib.load()
-    y = torch.empty(1, n, dtype=torch.float16, device=x.device)
-    rc = _lib.RopeCache(_ptr(cos), _ptr(sin), _ptr(pos), _ptr(cache_k), _ptr(cache_v), heads, kv_heads, head_dim,
-                        max_seq)
-    with _on(x.device):
-        status = lib.kf_int4_gemv_qkv_rope(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), n, k, int(group_size),
-                                           _ptr(norm_weight) if norm_weight is not None else None, float(eps),
-                                           ctypes.byref(rc), _stream_ptr(x.device))
-    _lib.check(status, "int4_gemv_qkv_rope")
+    args = (x2, packed, scales, int(group_size), cos, sin, pos, cache_k, cache_v, int(heads), int(kv_heads),
+            int(head_dim), norm_weight, float(eps))
+    y = _int4_qkv_rope_cache_op(*args) if _traced((x2, packed, scales, cos, sin, pos, cache_k, cache_v,
+                                                   norm_weight)) else _launch_qkv_rope(*args)
     return y.reshape(*x.shape[:-1], n)
+
+
+def _launch_qkv_rope(x2, packed, scales, group_size, cos, sin, pos, cache_k, cache_v, heads, kv_heads, head_dim,
+                     norm_weight, eps) -> torch.Tensor:
+    """kf_int4_gemv_qkv_rope on int4_qkv_rope_cache's validated inputs; y [1, N]."""
+    _check_native(x2, packed, scales, group_size)
+    for name, t in (("cos", cos), ("sin", sin), ("pos", pos), ("cache_k", cache_k), ("cache_v", cache_v),
+                    ("norm_weight", norm_weight)):
+        if t is not None and (isinstance(t, FakeTensor) or t.is_meta):
+            raise RuntimeError(f"{name} has no device memory (a fake or meta tensor)")
+    if norm_weight is not None and norm_weight.data_ptr() % 16:
+        raise ValueError(f"norm_weight must be a contiguous, 16-byte aligned fp16 [{x2.shape[1]}]")
+    lib = _lib.load()
+    n, k = packed.shape[0], x2.shape[1]
+    y = torch.empty(1, n, dtype=torch.float16, device=x2.device)
+    rc = _lib.RopeCache(_ptr(cos), _ptr(sin), _ptr(pos), _ptr(cache_k), _ptr(cache_v), heads, kv_heads, head_dim,
+                        cos.shape[0])
+    with _on(x2.device):
+        status = lib.kf_int4_gemv_qkv_rope(_ptr(x2), _ptr(packed), _ptr(scales), _ptr(y), n, k, group_size,
+                                           _ptr(norm_weight) if norm_weight is not None else None, eps,
+                                           ctypes.byref(rc), _stream_ptr(x2.device))
+    _lib.check(status, "int4_gemv_qkv_rope")
+    return y
+
+
+@torch.library.custom_op("kernelforge::int4_qkv_rope_cache", mutates_args=("cache_k", "cache_v"))
+def _int4_qkv_rope_cache_op(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group_size: int,
+                            cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor, cache_k: torch.Tensor,
+                            cache_v: torch.Tensor, heads: int, kv_heads: int, head_dim: int,
+                            norm_weight: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    return _launch_qkv_rope(x, packed, scales, group_size, cos, sin, pos, cache_k, cache_v, heads, kv_heads,
+                            head_dim, norm_weight, eps)
+
+
+@_int4_qkv_rope_cache_op.register_fake
+def _(x, packed, scales, group_size, cos, sin, pos, cache_k, cache_v, heads, kv_heads, head_dim, norm_weight, eps):
+    return x.new_empty(1, packed.shape[0])
 

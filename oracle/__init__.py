@@ -11,6 +11,9 @@ package never imports it.
   cpu_baseline.py  the reference's CPU FP32 dequant + matmul in torch (bench.py's cpu_baseline leg)
 
 Every function is pinned in tests/test_oracle.py (KATs, exact rational arithmetic, brute force,
-the C restatement; quantization_error on a crafted weight with exact errors); none is
-"parity unpinned".
+the C restatement; quantization_error on a crafted weight with exact errors).  The pass rule
+itself, max_rel_err (numpy) and kfo_max_rel_err_f16 (C, used by the native check), is pinned by
+hand-computed dyadic cases that each plausible misreading fails: a per-element ratio, a mean, a
+missing abs, a scale taken from out, a per-row scale, a dropped NaN, an all-zero ref, a shape
+mismatch.  No function is left "parity unpinned".
 """

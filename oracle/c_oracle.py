@@ -36,6 +36,8 @@ def load():
         lib.kfo_lcg_workload.argtypes = [I, I, I, P, I, P, P, P, P]
         lib.kfo_dequant_fp16.argtypes = [P, P, I, I, I, P]
         lib.kfo_ref_f64.argtypes = [P, P, P, I, I, I, I, P]
+        lib.kfo_max_rel_err_f16.restype = ctypes.c_double
+        lib.kfo_max_rel_err_f16.argtypes = [P, P, ctypes.c_size_t]
         _lib = lib
     return _lib
 
@@ -98,3 +100,12 @@ def ref_f64(x16: np.ndarray, packed: np.ndarray, scales: np.ndarray, group: int)
     y = np.zeros((m, n), dtype=np.float64)
     load().kfo_ref_f64(_p(x), _p(packed), _p(sc), m, n, k, group, _p(y))
     return y
+
+
+def max_rel_err_f16(y16: np.ndarray, ref: np.ndarray) -> float:
+    """kfo_max_rel_err_f16: the native check's pass-rule ratio of fp16 outputs against a float64 ref."""
+    y = np.ascontiguousarray(y16, dtype=np.float16).view(np.uint16).ravel()
+    r = np.ascontiguousarray(ref, dtype=np.float64).ravel()
+    if y.size != r.size:
+        raise ValueError("max_rel_err_f16: sizes differ")
+    return float(load().kfo_max_rel_err_f16(_p(y), _p(r), y.size))

@@ -170,12 +170,28 @@ def linear_ref_f64(x16: np.ndarray, packed: np.ndarray, scales: np.ndarray, grou
 
 
 def max_rel_err(out: np.ndarray, ref: np.ndarray) -> float:
-    """tests/test_gemm.py:39-42: max|out - ref| / max|ref| over the whole tensor."""
+    """tests/test_gemm.py:39-42: max|out - ref| / max|ref|, both maxima over the whole tensor.
+
+    The reference passes a case when err <= tol * scale; this returns the ratio so that
+    ``max_rel_err(out, ref) <= tol`` decides exactly the same way:
+      * a NaN anywhere in out (or ref) gives NaN, which fails every ``<=`` test;
+      * an all-zero ref passes only an exactly-zero error (0 for err == 0, else inf);
+      * out and ref must have one shape (no broadcasting of a transposed or flattened out);
+      * an empty tensor has no error (0).
+    """
     out = np.asarray(out, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
-    scale = float(np.abs(ref).max()) if ref.size else 0.0
-    err = float(np.abs(out - ref).max()) if ref.size else 0.0
-    return err / scale if scale > 0 else err
+    if out.shape != ref.shape:
+        raise ValueError(f"max_rel_err: out {out.shape} and ref {ref.shape} differ in shape")
+    if ref.size == 0:
+        return 0.0
+    err = float(np.max(np.abs(out - ref)))
+    scale = float(np.max(np.abs(ref)))
+    if np.isnan(err) or np.isnan(scale):
+        return float("nan")
+    if scale == 0.0:
+        return 0.0 if err == 0.0 else float("inf")
+    return err / scale
 
 
 class Lcg:

@@ -9,6 +9,7 @@
  *   kfo_unpack         kernelforge/quantize.py:88-97
  *   kfo_dequant_fp16   kernelforge/quantize.py:112-113 (fp16(q * s), one RNE)
  *   kfo_ref_f64        csrc/micro/sanitize_gemm.cu:58-66 (double-precision sum)
+ *   kfo_max_rel_err_f16 tests/test_gemm.py:36-45 (pass rule; the native check's)
  *   kfo_f32_to_f16     IEEE 754 binary32 -> binary16, round to nearest even,
  *                      written from the format definition (no library call)
  *
@@ -18,6 +19,7 @@
  * changes the fp32 arithmetic of uniform() and the scale formula).
  */
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -115,6 +117,24 @@ void kfo_dequant_fp16(const int32_t* packed, const uint16_t* scales, int n, int 
         out[(size_t)r * k + 8 * w + kNibbleK[i]] = kfo_f32_to_f16((float)q * s);
       }
     }
+}
+
+/* The pass rule of tests/test_gemm.py:36-45 (and sanitize_gemm.cu:84-86) on fp16 outputs:
+ * max|y - ref| / max|ref| over all n elements, so that "result <= tol" decides as the
+ * reference's "err <= tol * scale" does.  A NaN in y or ref gives NaN (fails every <= test;
+ * fmax would drop it), an all-zero ref gives 0 for a zero error and +inf otherwise, n == 0
+ * gives 0. */
+double kfo_max_rel_err_f16(const uint16_t* y, const double* ref, size_t n) {
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    const double d = fabs((double)kfo_f16_to_f32(y[i]) - ref[i]);
+    const double a = fabs(ref[i]);
+    if (isnan(d) || isnan(a)) return NAN;
+    if (d > num) num = d;
+    if (a > den) den = a;
+  }
+  if (den == 0.0) return num == 0.0 ? 0.0 : INFINITY;
+  return num / den;
 }
 
 void kfo_ref_f64(const uint16_t* x, const int32_t* packed, const uint16_t* scales, int m, int n, int k,

@@ -27,6 +27,7 @@ void kfo_ref_f64(const uint16_t* x, const int32_t* packed, const uint16_t* scale
                  double* y);
 float kfo_f16_to_f32(uint16_t h);
 uint16_t kfo_f32_to_f16(float f);
+double kfo_max_rel_err_f16(const uint16_t* y, const double* ref, size_t n);
 }
 
 namespace {
@@ -99,13 +100,11 @@ class EventTimer {
 constexpr uint16_t kGuard = 0x7E11;  // an fp16 NaN pattern the kernels never produce
 constexpr int kGuardElems = 64;
 
+// The pass rule's ratio from the C oracle (kfo_max_rel_err_f16, pinned by tests/test_oracle.py):
+// NaN for a NaN output, so "err <= 2e-3" fails on it.
 double max_rel_err(const std::vector<uint16_t>& y, const std::vector<double>& ref) {
-  double num = 0.0, den = 0.0;
-  for (size_t i = 0; i < ref.size(); ++i) {
-    num = std::fmax(num, std::fabs((double)kfo_f16_to_f32(y[i]) - ref[i]));
-    den = std::fmax(den, std::fabs(ref[i]));
-  }
-  return num / (den > 0.0 ? den : 1.0);
+  if (y.size() < ref.size()) return NAN;
+  return kfo_max_rel_err_f16(y.data(), ref.data(), ref.size());
 }
 
 void run_group(int group, hipStream_t stream) {

@@ -142,6 +142,24 @@ def test_other_sizes_run_the_torch_composition(m, k):
     assert torch.equal(got, ops.int4_linear(torch.nn.functional.silu(x) * u, dp, ds, G))
 
 
+def test_misaligned_operands_take_the_composition():
+    """x or the SwiGLU up operand 2 bytes off a 16-byte boundary (one-row views into a larger
+    buffer): the launch's LDS copies cannot take them, so the result is the torch composition's."""
+    n, k = 2048, 2048
+    _, _, dp, ds = _weight(n, k)
+    buf = _h(_rng(51).standard_normal((1, k + 8)))
+    x = buf[:, 1:k + 1]
+    assert x.is_contiguous() and x.data_ptr() % 16 == 2
+    w = _h(_rng(52).uniform(0.5, 1.5, k))
+    got = ops.int4_linear_fused(x, dp, ds, G, norm_weight=w)
+    assert torch.equal(got, ops.int4_linear(torch.nn.functional.rms_norm(x, (k,), w, 1e-5), dp, ds, G))
+    g = _h(_rng(53).standard_normal((1, k)))
+    up = buf[:, 1:k + 1]
+    r = _h(_rng(54).standard_normal((1, n)))
+    got = ops.int4_linear_fused(g, dp, ds, G, up=up, residual=r)
+    assert torch.equal(got, r + ops.int4_linear(torch.nn.functional.silu(g) * up, dp, ds, G))
+
+
 def test_graph_replays_equal_eager():
     n, k = 2048, 5632
     _, _, dp, ds = _weight(n, k)

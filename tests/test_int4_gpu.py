@@ -204,6 +204,41 @@ def test_grouped_qwen_seven_as_benchmarked(error_log, group):
         assert err <= REL_TOL, f"qwen {name}: {err:.3e}"
 
 
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_tinyllama_seven_as_benchmarked(error_log, group):
+    """BASELINE config 2 exactly as bench.py times its headline: bench.py's layer table and seeded
+    weights (make_layers), and one launch of bench.BoundSteps, which calls kf_int4_gemv_grouped
+    through the C ABI with the problem table the timed region uses.  The plan must be the one the
+    headline runs (gate at three rows per wavefront, the rest at two, x in LDS); every output must
+    equal ops.int4_linear_grouped's and its own GEMV launch bit for bit, and the oracle within the
+    reference's tolerance."""
+    import bench
+    from kernelforge import quantize as kq_
+
+    shapes = [(n, k) for _, n, k in bench.TL_LAYERS]
+    assert [nm for nm, _, _ in bench.TL_LAYERS] == ["q", "k", "v", "o", "gate", "up", "down"]
+    plan = _lib.gemv_plan(1, shapes)
+    assert plan["rows"] == [2, 2, 2, 2, 3, 2, 2] and plan["x_lds"], plan
+    layers = bench.make_layers(torch, kq_, bench.TL_LAYERS, group=group)
+    xs = [ly["x"].to(DEV) for ly in layers]
+    dev = [[(ly["packed"].to(DEV), ly["scales"].to(DEV)) for ly in layers]]
+    steps = bench.BoundSteps(torch, _lib, _lib.load(), xs, dev, group)
+    print(f"tinyllama seven as benchmarked: G={group} plan {plan}", flush=True)
+    steps.launch(0)
+    torch.cuda.synchronize()
+    via_op = ops.int4_linear_grouped(xs, [p for p, _ in dev[0]], [s for _, s in dev[0]], group)
+    for i, ly in enumerate(layers):
+        y = steps.ys[i]
+        assert torch.equal(y, via_op[i]), f"{ly['name']}: BoundSteps launch != int4_linear_grouped"
+        assert torch.equal(y, ops.int4_gemv(xs[i], *dev[0][i], group)), f"{ly['name']}: grouped != single"
+        packed, scales = ly["packed"].numpy(), ly["scales"].numpy()
+        ref = o.linear_ref_fp32(ly["x"].numpy(), packed, scales, group)
+        err = o.max_rel_err(y.float().cpu().numpy(), ref)
+        error_log.add("int4_gemv_grouped", case=f"tinyllama_seven_{ly['name']}", shape=[1, ly["N"], ly["K"]],
+                      group=group, max_rel_err=err, passed=err <= REL_TOL)
+        assert err <= REL_TOL, f"tinyllama {ly['name']}: {err:.3e}"
+
+
 @pytest.mark.parametrize("shapes,m_leads", [
     ([(9, 256), (129, 512), (64, 4160), (1, 128)], [(1, 1), (2, 3)]),  # ragged N at M <= 8: GEMV fallback
     ([(64, 256), (192, 512), (128, 4160)], [(2, 5), (33,)]),            # M > GEMV_MAX_M: per-problem GEMM

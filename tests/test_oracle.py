@@ -280,6 +280,75 @@ def test_linear_refs_against_brute_force_loop():
     assert o.max_rel_err(o.linear_ref_fp32(x, packed, scales, g), brute) < 1e-5
 
 
+# The pass rule every GPU parity assertion goes through (tests/test_gemm.py:36-45: err <= 2e-3 *
+# scale, err = max|out - ref|, scale = max|ref|, both over the whole tensor).  Every value is a
+# dyadic rational, exact in fp16 and float64, so each expected ratio is exact.  In the first case
+# the largest error is negative and sits at another element than the largest |ref|, which is
+# negative too; the wrong readings each give another number:
+#   per-element |e|/|ref| -> 1.0; mean |e| -> 0.1042; max(out - ref) without abs -> 0.125;
+#   scale from out -> 0.1786; max(ref) without abs -> 0.3125; rms of e -> 0.1169.
+# The second case puts the error and the largest |ref| in different rows and columns (a
+# per-row or per-column scale gives 1.0).
+_NAN = object()
+MAX_REL_ERR_CASES = [
+    ("negatives_apart", [0.25, 1.375, -3.5], [0.125, 2.0, -4.0], 0.15625),
+    ("two_d_whole_tensor", [[1.0, 0.25], [0.25, -8.0]], [[0.5, 0.25], [0.25, -8.0]], 0.0625),
+    ("exact", [[-1.5, 0.75]], [[-1.5, 0.75]], 0.0),
+    ("nan_beside_exact", [np.nan, 1.0], [1.0, 1.0], _NAN),      # fmax would drop the NaN: 0.0
+    ("nan_beside_error", [0.5, np.nan, 2.0], [0.5, 1.0, 1.0], _NAN),
+    ("inf_out", [np.inf, 1.0], [1.0, 1.0], float("inf")),
+    ("zero_ref_exact", [0.0, -0.0, 0.0], [0.0, 0.0, 0.0], 0.0),
+    ("zero_ref_tiny_error", [0.0, 2.0 ** -24], [0.0, 0.0], float("inf")),  # the reference fails it
+]
+
+
+@pytest.mark.parametrize("name,out,ref,want", MAX_REL_ERR_CASES, ids=[c[0] for c in MAX_REL_ERR_CASES])
+def test_max_rel_err_hand_computed(name, out, ref, want):
+    """oracle.max_rel_err and the native check's kfo_max_rel_err_f16 on hand-computed cases, and
+    the pass decision (<= 2e-3) equal to the reference's err <= 2e-3 * scale."""
+    out64 = np.array(out, dtype=np.float64)
+    ref64 = np.array(ref, dtype=np.float64)
+    got_np = o.max_rel_err(out64, ref64)
+    got_c = c_oracle.max_rel_err_f16(out64.astype(np.float16), ref64)
+    for got in (got_np, got_c):
+        if want is _NAN:
+            assert np.isnan(got), name
+        else:
+            assert got == want, (name, got)
+    with np.errstate(invalid="ignore"):
+        err = np.max(np.abs(out64 - ref64))
+        ref_pass = bool(err <= 2e-3 * np.max(np.abs(ref64)))
+    assert (got_np <= 2e-3) == ref_pass == (got_c <= 2e-3), name
+
+
+def test_max_rel_err_refuses_shape_mismatch_and_empty_is_zero():
+    """A transposed or flattened out must not broadcast against ref into an N x N difference."""
+    with pytest.raises(ValueError, match="shape"):
+        o.max_rel_err(np.zeros((1, 3)), np.zeros((3, 1)))
+    with pytest.raises(ValueError, match="shape"):
+        o.max_rel_err(np.zeros(3), np.zeros((1, 3)))
+    assert o.max_rel_err(np.zeros((0, 4)), np.zeros((0, 4))) == 0.0
+    assert c_oracle.max_rel_err_f16(np.zeros(0, np.float16), np.zeros(0)) == 0.0
+
+
+def test_max_rel_err_on_a_gemv_sized_output():
+    """A seeded [1, 5632] output: one element off by exactly 2e-3 * max|ref| (+/- a little) decides
+    pass / fail at the reference's boundary, in both implementations."""
+    rng = np.random.default_rng(11)
+    ref = rng.standard_normal((1, 5632))
+    out16 = ref.astype(np.float16)
+    base = o.max_rel_err(out16.astype(np.float64), ref)
+    assert base < 2.0 ** -11 and c_oracle.max_rel_err_f16(out16, ref) == base
+    scale = np.abs(ref).max()
+    j = int(np.argmin(np.abs(ref)))  # far from the largest |ref|
+    for factor, passes in ((0.9, True), (1.1, False)):
+        bad = ref.copy()
+        bad[0, j] += factor * 2e-3 * scale
+        bad16 = bad.astype(np.float16)
+        assert (o.max_rel_err(bad16.astype(np.float64), ref) <= 2e-3) is passes
+        assert (c_oracle.max_rel_err_f16(bad16, ref) <= 2e-3) is passes
+
+
 def test_linear_ref_is_linear_in_x():
     rng = np.random.default_rng(6)
     w = (rng.standard_normal((64, 256)) * 0.02).astype(np.float32)

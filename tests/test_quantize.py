@@ -1,12 +1,14 @@
 """The package's format producer (kernelforge.quantize, torch) against the pinned oracle.
 
-Restates the reference's tests/test_quantize.py (KATs, invariants, rejections)
-for the package, and checks that its packed bytes and scales are bit-identical
-to the numpy oracle on seeded, crafted and golden inputs.
+The reference's quantizer checks (tests/test_quantize.py:9-66: layout KAT, quantizer KAT,
+error invariants, rejections) are data in tests/golden/reference_kats.json; the tests below
+read them from there.  The packed bytes and scales are also checked bit for bit against the
+numpy oracle on seeded, crafted and golden inputs.
 """
 
 from __future__ import annotations
 
+import json
 from pathlib import Path
 
 import numpy as np
@@ -17,6 +19,7 @@ from kernelforge import quantize as kq
 from oracle import int4_oracle as o
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "int4_cases.npz"
+KATS = json.loads((Path(__file__).resolve().parent / "golden" / "reference_kats.json").read_text())
 
 
 def _cases():
@@ -25,32 +28,79 @@ def _cases():
     return data, names
 
 
-def test_pack_unpack_roundtrip_is_exact():
-    g = torch.Generator().manual_seed(0)
-    q = torch.randint(-8, 8, (64, 256), generator=g, dtype=torch.int8)
-    assert torch.equal(kq.unpack_int4(kq.pack_int4(q)), q)
+def _nibbles(word: int) -> list[int]:
+    return [(word >> (4 * i)) & 0xF for i in range(8)]
 
 
-def test_bit_layout_matches_docstring():
-    q = torch.arange(0, 8, dtype=torch.int8).reshape(1, 8)
-    word = kq.pack_int4(q).item() & 0xFFFFFFFF
-    assert [(word >> (4 * i)) & 0xF for i in range(8)] == [8, 10, 12, 14, 9, 11, 13, 15]
-    for i in range(4):
-        pair = (word >> (4 * i)) & 0x000F000F
-        assert (pair & 0xF, pair >> 16) == (2 * i + 8, 2 * i + 9)
+def test_layout_kat_from_fixture():
+    """pack_int4 of the fixture's q gives its word and nibble order; the (k 2i, k 2i+1) pairs a
+    kernel reads with one mask sit in the two 16-bit halves; unpack_int4 inverts it."""
+    kat = KATS["bit_layout"]
+    q = torch.tensor([kat["q"]], dtype=torch.int8)
+    packed = kq.pack_int4(q)
+    assert packed.dtype == torch.int32 and packed.shape == (1, 1)
+    assert packed.item() == kat["word_int32"]
+    word = packed.item() & 0xFFFFFFFF
+    assert word == int(kat["word_hex"], 16) and _nibbles(word) == kat["nibbles"]
+    halves = [((word >> (4 * i)) & 0xF, (word >> (4 * i + 16)) & 0xF) for i in range(4)]
+    assert halves == [(kat["q"][2 * i] + 8, kat["q"][2 * i + 1] + 8) for i in range(4)]
+    assert torch.equal(kq.unpack_int4(packed), q)
 
 
-@pytest.mark.parametrize("group_size", [64, 128])
-def test_quantization_error_is_bounded(group_size):
-    g = torch.Generator().manual_seed(1)
-    w = torch.randn(256, 1024, generator=g) * 0.02
-    qw = kq.quantize_weight(w, group_size)
-    w_hat = kq.dequantize(qw, torch.float32)
-    step = qw.scales.float().repeat_interleave(group_size, dim=1)
-    assert ((w_hat - w).abs() <= 0.5 * step + 1e-8).all()
+@pytest.mark.parametrize("pos", range(8))
+def test_every_value_at_every_nibble_round_trips(pos):
+    """Exhaustive over the 16 values at each of the 8 positions of a word, against the oracle's
+    packer, with every other k at q = 0 (nibble 8)."""
+    koff = o.NIBBLE_K[pos]
+    q = torch.zeros(16, 8, dtype=torch.int8)
+    q[:, koff] = torch.arange(-8, 8, dtype=torch.int8)
+    packed = kq.pack_int4(q)
+    assert np.array_equal(packed.numpy(), o.pack_int4(q.numpy()))
+    for u in range(16):
+        nib = _nibbles(int(packed[u, 0]) & 0xFFFFFFFF)
+        assert nib[pos] == u and all(v == 8 for i, v in enumerate(nib) if i != pos)
+    assert torch.equal(kq.unpack_int4(packed), q)
+
+
+def test_quantizer_kat_from_fixture():
+    """Row 0 holds only the fixture's nonzero entries, row 1 is all zeros (one group of 128 each)."""
+    kat = KATS["quantizer"]
+    w = torch.zeros(2, 128)
+    for idx, val in kat["row0_nonzero"]:
+        w[0, idx] = val
+    q, s = kq.quantize_int4(w, 128)
+    assert s.dtype == torch.float16 and s.shape == (2, 1)
+    assert int(q[0, 5]) == kat["q_row0_idx5"] and int(q[0, 9]) == kat["q_row0_idx9"]
+    assert float(s[0, 0]) == kat["scale_row0"] and float(s[1, 0]) == kat["scale_zero_group"]
+    others = [i for i in range(128) if i not in {idx for idx, _ in kat["row0_nonzero"]}]
+    assert not q[0, others].any() and not q[1].any()
+
+
+@pytest.mark.parametrize("group", KATS["invariants"]["groups"])
+def test_error_invariants_from_fixture(group):
+    """The fixture's bounds on a seeded weight of its shape: every element within the stated
+    fraction of its group's step (in float64; one part in 2^20 for the fp32 division), the
+    relative Frobenius error below its bound, the stated bits per weight."""
+    inv = KATS["invariants"]
+    shape = (inv["weight"]["rows"], inv["weight"]["cols"])
+    w = torch.randn(*shape, generator=torch.Generator().manual_seed(100 + group)) * inv["weight"]["std"]
+    qw = kq.quantize_weight(w, group)
+    err = (kq.dequantize(qw, torch.float32).double() - w.double()).abs()
+    step = qw.scales.double().repeat_interleave(group, dim=1)
+    assert bool((err <= inv["max_err_in_steps"] * step * (1 + 2.0 ** -20)).all())
     stats = kq.quantization_error(w, qw)
-    assert stats["rel_fro_err"] < 0.15
-    assert stats["bits_per_weight"] == pytest.approx(4 + 16 / group_size)
+    assert stats["rel_fro_err"] < inv["rel_fro_err_below"]
+    assert stats["bits_per_weight"] == inv["bits_per_weight"][str(group)]
+
+
+@pytest.mark.parametrize("case", KATS["rejections"]["cases"], ids=lambda c: f"{c['call']}-{c['match']}")
+def test_rejections_from_fixture(case):
+    err = {"ValueError": ValueError, "TypeError": TypeError}[case["error"]]
+    with pytest.raises(err, match=case["match"]):
+        if case["call"] == "quantize_weight":
+            kq.quantize_weight(torch.zeros(case["shape"]), case["group"])
+        else:
+            kq.pack_int4(torch.full(case["shape"], case["fill"], dtype=torch.int8))
 
 
 def test_quantization_error_matches_oracle_and_exact_values():
@@ -80,26 +130,6 @@ def test_quantization_error_matches_oracle_and_exact_values():
         for key in ("rmse", "rel_fro_err"):
             assert a[key] == pytest.approx(b[key], rel=1e-5)
         assert a["bits_per_weight"] == b["bits_per_weight"]
-
-
-def test_absmax_maps_to_seven_and_zero_groups_are_safe():
-    w = torch.zeros(2, 128)
-    w[0, 5] = -3.5
-    w[0, 9] = 1.0
-    q, s = kq.quantize_int4(w, 128)
-    assert q[0, 5].item() == -7 and s[0, 0].item() == 0.5
-    assert (q[1] == 0).all() and s[1, 0].item() == 1.0
-
-
-def test_rejections():
-    with pytest.raises(ValueError, match="not a multiple of group_size"):
-        kq.quantize_weight(torch.randn(16, 200), 128)
-    with pytest.raises(ValueError, match="group_size"):
-        kq.quantize_weight(torch.randn(16, 256), 32)
-    with pytest.raises(ValueError, match="2-D"):
-        kq.quantize_weight(torch.randn(4, 16, 256), 128)
-    with pytest.raises(ValueError, match=r"\[-8, 7\]"):
-        kq.pack_int4(torch.full((1, 8), 9, dtype=torch.int8))
 
 
 @pytest.mark.parametrize("seed,n,k,g", [(0, 64, 256, 64), (1, 33, 512, 128), (2, 256, 2048, 128),
