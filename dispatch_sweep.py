@@ -8,7 +8,9 @@ the largest M at which the sum of GEMV times over the shapes is below the sum of
 With ``--fp16`` it also times ``F.linear`` on fp16 weights of the same shape (hipBLASLt), the
 baseline the reference's bench/bench_gemm.py:83 calls ``cublas_fp16``.
 
-    python kernel-forge_amd/kernelforge/dispatch_sweep.py [--out sweep.json] [--ms 1,2,4,8,16] [--fp16]
+    python dispatch_sweep.py [--out sweep.json] [--ms 1,2,4,8,16] [--fp16] [--mfma16]
+
+A measurement harness beside bench.py, not part of the package.
 """
 
 from __future__ import annotations
@@ -20,7 +22,7 @@ from pathlib import Path
 
 import torch
 
-sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+sys.path.insert(0, str(Path(__file__).resolve().parent / "kernel-forge_amd"))
 
 from kernelforge import ops  # noqa: E402
 from kernelforge import quantize as kq  # noqa: E402
@@ -111,11 +113,11 @@ def main() -> None:
     ap.add_argument("--shapes", default=",".join(SHAPES))
     ap.add_argument("--out", default=None)
     ap.add_argument("--fp16", action="store_true", help="also time F.linear on fp16 weights (hipBLASLt)")
-    ap.add_argument("--no-mfma16", action="store_true",
-                    help="int4_gemm on the public weight layout only (ops.MFMA16_CACHE = False)")
+    ap.add_argument("--mfma16", action="store_true",
+                    help="int4_gemm builds and reads the MFMA-16 weight copy (ops.MFMA16_CACHE = True); "
+                         "default: the public layout")
     args = ap.parse_args()
-    if args.no_mfma16:
-        ops.MFMA16_CACHE = False
+    ops.MFMA16_CACHE = bool(args.mfma16)
     ms = [int(v) for v in args.ms.split(",")]
     shapes = {s: SHAPES[s] for s in args.shapes.split(",")}
     res = sweep(ms, shapes, fp16=args.fp16)

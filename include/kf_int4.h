@@ -160,6 +160,8 @@ int kf_int4_gemm_plan(int M, int N, int K, int group_size, int* kernel, int* num
                       int* splits, int* block_m, int* block_n);
 
 /* MFMA dequant GEMM, any M >= 1, N % 64 == 0 and N <= KF_MAX_ROWS, K % G == 0, G in {64, 128}.
+ * x, packed and y 16-byte aligned (its epilogues store y in 8- and 16-byte vectors; the GEMV
+ * entry points need only 2-byte aligned y).
  * ws may be NULL when kf_int4_gemm_workspace_bytes() returned 0.
  * Replaces kf::gemm_tc::run (dequant_gemm_tc_kernel.cuh:203-211) and the
  * pybind entry _C.int4_gemm (csrc/bindings.cpp:26-27,

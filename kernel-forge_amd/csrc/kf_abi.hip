@@ -128,6 +128,9 @@ int gemm_entry(const void* x, const void* packed, const void* scales, const void
   if (st) return st;
   if (N % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs N to be a multiple of 64, got N=%d", N);
   if (K % 64 != 0) return fail(KF_ERR_UNSUPPORTED, "int4_gemm needs K to be a multiple of 64, got K=%d", K);
+  // The GEMM epilogues store y as 8- and 16-byte vectors (N % 64 == 0 keeps every row's start on
+  // a 16-byte boundary once y's is).
+  if (!aligned(y, 16)) return fail(KF_ERR_INVALID_ARG, "int4_gemm needs y to be 16-byte aligned");
   int cus = 0;
   if ((st = cu_count(&cus))) return st;
   const kf::GemmPlan plan = kf::gemm_plan(M, N, K, cus);

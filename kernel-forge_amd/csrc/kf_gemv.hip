@@ -987,7 +987,10 @@ GemvPlan gemv_plan(int M, const int* N, const int* K, int count, int cu_count) {
       // x past the default budget (M = 2 with K > 5120): in LDS after all when the launch, with
       // three rows per wavefront for every two-row problem, fits the workgroups the LDS holds;
       // the shaping below then aims at that many wave slots (TinyLlama's 7 linears: 22 KiB of x,
-      // seven workgroups per CU).
+      // seven workgroups per CU by LDS).  The mixed M = 2 kernel this selects holds only five
+      // 4-wavefront workgroups per CU by its registers (85 VGPRs, 5 waves per SIMD), so such a
+      // launch runs in about 1.4 rounds (TinyLlama: 7,088 wavefronts, 5,120 resident); measured on
+      // MI355X it is still faster than per-lane x loads in one round (8.63 -> 7.42 us).
       const long lds_slots = (long)(kLdsPerCu / xb) * kGemvWavesPerBlock * cus;
       long w3 = 0;
       for (int i = 0; i < count; ++i) {

@@ -22,7 +22,7 @@ from torch._subclasses.fake_tensor import FakeTensor
 
 from kernelforge import _lib
 
-# Measured GEMV/GEMM crossover on one MI355X (kernelforge/dispatch_sweep.py): the
+# Measured GEMV/GEMM crossover on one MI355X (dispatch_sweep.py beside bench.py): the
 # largest M at which the sum of GEMV times over the layer shapes beats the GEMM's
 # (reference rule, bench/sweep_int4_dispatch.py:51-57).  Above it int4_gemm runs the
 # skinny MFMA kernel for small M, then the tiled MFMA kernels.
@@ -152,11 +152,14 @@ def _launch_gemv(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, gr
 
 
 # The MFMA-16 block copy of a weight (kf_int4_reorder_mfma16) makes the skinny MFMA kernel's
-# weight loads contiguous (7-15% faster at M <= 32) and is bit-identical in results.  When
-# enabled, int4_gemm builds it the first time a weight is used at M <= MFMA16_MAX_M (outside
-# HIP-graph capture) and keeps it on the packed tensor, at the cost of a second copy of that
-# weight in device memory.
-MFMA16_CACHE = True
+# weight loads contiguous (7-15% faster at M <= 32) and is bit-identical in results, at the cost
+# of a second copy of the weight in device memory (0.74x the INT4 weights of a TinyLlama whose
+# layers all run the skinny kernel once) and one host wait when it is built.  Opt-in, two ways:
+# prepare_mfma16(packed, scales) attaches a copy to one weight, which int4_gemm then reads
+# whenever it runs the skinny kernel on it; MFMA16_CACHE = True makes int4_gemm build and attach
+# one by itself the first time any weight runs the skinny kernel at M <= MFMA16_MAX_M (outside
+# HIP-graph capture).  Off, the skinny kernel reads the public layout.
+MFMA16_CACHE = False
 MFMA16_MAX_M = 32
 _MFMA16_ATTR = "_kf_mfma16"
 
@@ -193,11 +196,13 @@ def _mfma16_key(packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> 
 def prepare_mfma16(packed: torch.Tensor, scales: torch.Tensor, group_size: int = 128) -> None:
     """Builds the MFMA-16 copy of a weight now and keeps it on `packed` for int4_gemm.
 
-    int4_gemm builds it by itself on first use, except for tensors created under
-    torch.inference_mode() (no version counter to notice in-place updates): for those this is
-    the only way, and the caller promises not to modify packed / scales in place afterwards.
-    Not during HIP-graph capture.  The host waits for the copy to be written before it is
-    attached, so a later int4_gemm on any stream reads a complete copy.
+    The per-weight opt-in: int4_gemm reads the copy whenever it runs the skinny kernel on this
+    weight (with MFMA16_CACHE on it would build one by itself on first use, except for tensors
+    created under torch.inference_mode(), which have no version counter to notice in-place
+    updates: for those this is the only way, and the caller promises not to modify packed /
+    scales in place afterwards).  An in-place update of a weight with version counters makes
+    int4_gemm ignore the stale copy.  Not during HIP-graph capture.  The host waits for the copy
+    to be written before it is attached, so a later int4_gemm on any stream reads a complete copy.
     """
     if torch.cuda.is_current_stream_capturing():
         raise RuntimeError("prepare_mfma16 launches a kernel and allocates; call it outside HIP-graph capture")
@@ -209,14 +214,17 @@ def prepare_mfma16(packed: torch.Tensor, scales: torch.Tensor, group_size: int =
 
 
 def _mfma16_copy(packed: torch.Tensor, scales: torch.Tensor, group_size: int, m: int):
-    """The cached MFMA-16 copy of (packed, scales), built on first use; None when not applicable."""
-    if not MFMA16_CACHE or m > MFMA16_MAX_M or packed.shape[1] % 16 != 0:
+    """The MFMA-16 copy of (packed, scales) attached by prepare_mfma16 (or, with MFMA16_CACHE, built
+    here on first use); None when there is none or it does not apply."""
+    if m > MFMA16_MAX_M or packed.shape[1] % 16 != 0:
+        return None
+    cached = getattr(packed, _MFMA16_ATTR, None)
+    if cached is None and not MFMA16_CACHE:
         return None
     key = _mfma16_key(packed, scales, group_size)
-    cached = getattr(packed, _MFMA16_ATTR, None)
     if cached is not None and cached[0] == key:
         return cached[1], cached[2]
-    if key[3] is None or torch.cuda.is_current_stream_capturing():
+    if not MFMA16_CACHE or key[3] is None or torch.cuda.is_current_stream_capturing():
         return None  # inference tensors: only a copy made by prepare_mfma16
     if gemm_plan(m, packed.shape[0], packed.shape[1] * 8, group_size, packed.device)["kernel"] != "skinny":
         return None  # only the skinny kernel reads the copy

@@ -88,6 +88,10 @@ def test_gemm_argument_errors_without_gpu():
     _err(lib.kf_int4_gemm(p, p, p, p, None, 0, 16, 100, 256, 128, None), "multiple of 64")
     _err(lib.kf_int4_gemm(p, p, None, p, None, 0, 16, 128, 256, 128, None), "non-null")
     _err(lib.kf_int4_gemm(p, p, p, p, None, 0, 16, 128, 320, 128, None), "not a multiple of group_size")
+    y2 = ctypes.c_void_p(0x1002)  # 2-byte aligned: enough for the GEMV, not for the GEMM's vector stores
+    _err(lib.kf_int4_gemm(p, p, p, y2, None, 0, 16, 128, 256, 128, None), "y to be 16-byte aligned")
+    _err(lib.kf_int4_gemm_noalloc(p, p, p, y2, 16, 128, 256, 128, None), "y to be 16-byte aligned")
+    _err(lib.kf_int4_gemm_mfma16(p, p, p, p, p, y2, None, 0, 16, 128, 256, 128, None), "y to be 16-byte aligned")
     _err(lib.kf_int4_dequant_fp16(None, p, p, 4, 256, 128, None), "non-null")
     _err(lib.kf_bw_copy(p, p, 17, 0, None), "multiple of 16")
     assert lib.kf_int4_gemm_workspace_bytes(0, 64, 256, 128) == 0

@@ -114,7 +114,27 @@ def test_op_cache_builds_reuses_and_invalidates():
         ops.MFMA16_CACHE = old
 
 
-def test_graph_capture_uses_cached_copy():
+def test_default_builds_no_copy_but_uses_a_prepared_one():
+    """The copy is opt-in: by default int4_gemm attaches nothing; a copy attached with
+    prepare_mfma16 is read (same bits) and ignored once the weight is updated in place."""
+    assert ops.MFMA16_CACHE is False
+    n, k, g = 2048, 2048, 128
+    _, _, dp, ds = _weight(n, k, g, seed=5)
+    x = torch.randn(8, k, device=DEV).half()
+    plain = ops.int4_gemm(x, dp, ds, g)
+    assert getattr(dp, "_kf_mfma16", None) is None
+    ops.prepare_mfma16(dp, ds, g)
+    copy = getattr(dp, "_kf_mfma16")
+    assert torch.equal(ops.int4_gemm(x, dp, ds, g), plain) and getattr(dp, "_kf_mfma16") is copy
+    _, _, dp2, ds2 = _weight(n, k, g, seed=6)
+    dp.copy_(dp2)
+    ds.copy_(ds2)
+    assert torch.equal(ops.int4_gemm(x, dp, ds, g), ops.int4_gemm(x, dp2, ds2, g))
+    assert getattr(dp, "_kf_mfma16") is copy  # stale, not rebuilt without MFMA16_CACHE, not read
+
+
+def test_graph_capture_uses_cached_copy(monkeypatch):
+    monkeypatch.setattr(ops, "MFMA16_CACHE", True)
     n, k, g = 5632, 2048, 128
     _, _, dp, ds = _weight(n, k, g)
     static_x = torch.randn(4, k, device=DEV).half()
