@@ -263,6 +263,80 @@ def e2e_decode(torch, prompt_len: int = 16, new_tokens: int = 128) -> dict:
     return out
 
 
+def hf_llama_decode(torch, prompt_len: int = 16, new_tokens: int = 64) -> dict:
+    """The reference's real caller at decode: a transformers LlamaForCausalLM of the TinyLlama
+    architecture (config 5's shapes, random init, SDPA attention, fp16), its 7 decoder linears
+    per layer swapped by quantize_linears_, decoded the way the reference's harness does
+    (bench/e2e_model.py:85-141: StaticCache, one decode step captured in a HIP graph, each replay
+    followed by the argmax copy, the position bump and a host sync; tokens/s = 1 / median step).
+    Three models: the INT4 modules as quantize_linears_ leaves them, the same after
+    group_sibling_linears_ (q|k|v and gate|up as one grouped launch each), and fp16 weights."""
+    import transformers
+    from transformers import StaticCache
+
+    from kernelforge import modules
+
+    dev = torch.device("cuda")
+    cfg = transformers.LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_hidden_layers=22,
+                                   num_attention_heads=32, num_key_value_heads=4, head_dim=64,
+                                   max_position_embeddings=2048, rms_norm_eps=1e-5, rope_theta=10000.0,
+                                   tie_word_embeddings=False, attn_implementation="sdpa")
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(7)).to(dev)
+    out = {"model": "transformers LlamaForCausalLM, tinyllama-1.1b-arch random-init, sdpa", "prompt": prompt_len,
+           "new_tokens": new_tokens, "protocol": "bench/e2e_model.py graph_decode: median step incl. argmax + sync"}
+
+    def graph_decode(model):
+        p = prompt.shape[1]
+        cache = StaticCache(config=model.config, max_cache_len=p + new_tokens + 8)
+        logits = model(prompt, cache_position=torch.arange(p, device=dev), past_key_values=cache, use_cache=True).logits
+        tok = logits[:, -1:].argmax(-1).clone()
+        tokens = [tok.item()]
+        pos = torch.tensor([p], device=dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                model(tok, cache_position=pos, past_key_values=cache, use_cache=True)
+        torch.cuda.current_stream().wait_stream(side)
+        for layer in cache.layers:
+            if hasattr(layer, "cumulative_length"):
+                layer.cumulative_length.fill_(p)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = model(tok, cache_position=pos, past_key_values=cache, use_cache=True).logits
+        times = []
+        for _ in range(new_tokens):
+            t = time.perf_counter()
+            graph.replay()
+            tok.copy_(logits[:, -1:].argmax(-1))
+            pos.add_(1)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t)
+            tokens.append(tok.item())
+        del graph, cache
+        med = statistics.median(times)
+        return round(1.0 / med, 1), round(med * 1e3, 4), tokens
+
+    with torch.no_grad():
+        torch.manual_seed(0)
+        with torch.device(dev):
+            model = transformers.LlamaForCausalLM(cfg)
+        model = model.half().eval()
+        fp16 = graph_decode(model)
+        out["fp16_tok_s"], out["fp16_step_ms"] = fp16[0], fp16[1]
+        modules.quantize_linears_(model, GROUP)
+        plain = graph_decode(model)
+        out["int4_tok_s"], out["int4_step_ms"] = plain[0], plain[1]
+        out["grouped_siblings"] = modules.group_sibling_linears_(model)
+        grouped = graph_decode(model)
+        out["int4_grouped_tok_s"], out["int4_grouped_step_ms"] = grouped[0], grouped[1]
+        out["grouped_tokens_equal_ungrouped"] = grouped[2] == plain[2]
+        out["first_tokens"] = plain[2][:8]
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def mfma16_copy_report(model) -> dict:
     """Device memory of the MFMA-16 weight copies int4_gemm attached to the model's INT4 weights
     (built on the first skinny-kernel call per weight: here the 16-token prefill), against the
@@ -923,6 +997,13 @@ def main() -> int:
         e2e = e2e_decode(torch)
         log(f"decode tok/s: int4 fused {e2e['int4_fused_tok_s']}, unfused {e2e['int4_unfused_tok_s']}, "
             f"fp16 {e2e['fp16_tok_s']}")
+        try:
+            log("HF LlamaForCausalLM graph decode leg")
+            e2e["hf_llama"] = hf_llama_decode(torch)
+            h = e2e["hf_llama"]
+            log(f"HF decode tok/s: int4 {h['int4_tok_s']}, grouped {h['int4_grouped_tok_s']}, fp16 {h['fp16_tok_s']}")
+        except ImportError as exc:
+            e2e["hf_llama"] = f"unavailable: {exc}"
 
     # --- CPU baseline: the reference's FP32 dequant + matmul on the host cores ------------------
     cpu = None

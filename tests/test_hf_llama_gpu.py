@@ -10,7 +10,9 @@ The model is random-init from a small LlamaConfig (no download): 2 layers, hidde
 * prompt logits against the same network in fp32 on the CPU with W_hat = q * s from the oracle
   (2e-2 relative rule, same argmax: only activation precision differs);
 * greedy tokens from graph replays equal eager StaticCache decode (the reference's check);
-* the last decode step's logits against the CPU fp32 model over the whole sequence.
+* the last decode step's logits against the CPU fp32 model over the whole sequence;
+* group_sibling_linears_ (q/k/v and gate/up of every layer in one grouped launch each): the
+  same logits and tokens as the ungrouped model, bit for bit, eager and from the graph.
 """
 
 from __future__ import annotations
@@ -84,15 +86,13 @@ def test_prompt_logits_match_cpu_fp32_reference():
     assert torch.equal(got.float().cpu().argmax(-1), ref.argmax(-1))
 
 
-@torch.no_grad()
-def test_graph_decode_equals_eager_static_cache_and_cpu_reference():
+def _decode(model, prompt, steps: int):
+    """Greedy decode the reference's way (bench/e2e_model.py:85-162): eager on a StaticCache, then
+    from a HIP graph of one decode step replayed with a device-side position.  Returns the eager
+    tokens, the graph tokens, and the last step's eager and graph logits."""
     from transformers import StaticCache
 
-    model = _int4_model(1)
-    p, steps = 12, 16
-    prompt = _prompt(p, seed=12).to(DEV)
-
-    # Eager decode on a StaticCache: the exact reference for the graph (same cache, masks, kernels).
+    p = prompt.shape[1]
     cache = StaticCache(config=model.config, max_cache_len=p + steps + 8)
     out = model(prompt, cache_position=torch.arange(p, device=DEV), past_key_values=cache, use_cache=True)
     t = out.logits[:, -1:].argmax(-1)
@@ -103,7 +103,6 @@ def test_graph_decode_equals_eager_static_cache_and_cpu_reference():
         eager.append(t.item())
     last_eager_logits = out.logits[0, -1].clone()
 
-    # One decode step captured in a HIP graph, replayed with a device-side position.
     cache = StaticCache(config=model.config, max_cache_len=p + steps + 8)
     out = model(prompt, cache_position=torch.arange(p, device=DEV), past_key_values=cache, use_cache=True)
     tok = out.logits[:, -1:].argmax(-1).clone()
@@ -127,8 +126,17 @@ def test_graph_decode_equals_eager_static_cache_and_cpu_reference():
         pos.add_(1)
         graph_tokens.append(tok.item())
     torch.cuda.synchronize()
+    return eager, graph_tokens, last_eager_logits, logits[0, -1].clone()
+
+
+@torch.no_grad()
+def test_graph_decode_equals_eager_static_cache_and_cpu_reference():
+    model = _int4_model(1)
+    steps = 16
+    prompt = _prompt(12, seed=12).to(DEV)
+    eager, graph_tokens, last_eager_logits, last_graph_logits = _decode(model, prompt, steps)
     assert graph_tokens == eager, f"graph {graph_tokens} vs eager {eager}"
-    assert torch.equal(logits[0, -1], last_eager_logits)
+    assert torch.equal(last_graph_logits, last_eager_logits)
 
     # The last step's logits against the CPU fp32 model run over the whole sequence.
     seq = torch.cat([prompt.cpu(), torch.tensor([eager[:steps]])], dim=1)
@@ -136,3 +144,32 @@ def test_graph_decode_equals_eager_static_cache_and_cpu_reference():
     rel = _rel(last_eager_logits, ref)
     assert rel < 2e-2, f"decode logits rel err {rel:.3e}"
     assert last_eager_logits.float().cpu().argmax() == ref.argmax()
+
+
+@torch.no_grad()
+def test_grouped_siblings_equal_ungrouped_model(monkeypatch):
+    """group_sibling_linears_ on the HF model: q/k/v and gate/up of every layer share one grouped
+    launch (counted on an eager decode step); prompt logits, eager and graph-decoded tokens and the
+    last logits equal the ungrouped model's bit for bit, and the CPU fp32 model within 2e-2."""
+    from kernelforge import modules, ops
+
+    plain, grouped = _int4_model(3), _int4_model(3)
+    assert modules.group_sibling_linears_(grouped) == 2 * LAYERS
+    prompt = _prompt(12, seed=13).to(DEV)
+    assert torch.equal(grouped(prompt).logits, plain(prompt).logits)
+
+    calls = []
+    real = ops.int4_linear_grouped
+    monkeypatch.setattr(ops, "int4_linear_grouped", lambda *a, **k: calls.append(len(a[0])) or real(*a, **k))
+    grouped(prompt[:, :1])
+    assert calls == [3, 2] * LAYERS, calls
+    monkeypatch.setattr(ops, "int4_linear_grouped", real)
+
+    steps = 12
+    want = _decode(plain, prompt, steps)
+    got = _decode(grouped, prompt, steps)
+    assert got[0] == want[0] and got[1] == want[1] == want[0], (got[:2], want[:2])
+    assert torch.equal(got[2], want[2]) and torch.equal(got[3], want[3])
+    seq = torch.cat([prompt.cpu(), torch.tensor([got[0][:steps]])], dim=1)
+    ref = _cpu_reference(grouped)(seq).logits[0, -1]
+    assert _rel(got[2], ref) < 2e-2 and got[2].float().cpu().argmax() == ref.argmax()
