@@ -142,14 +142,15 @@ class Attention(nn.Module):
             return y[..., :nqk], y[..., nqk:]
         return torch.cat([self.q_proj(x), self.k_proj(x)], dim=-1), self.v_proj(x)
 
-    def core(self, qk, v, pos, cos, sin, cache_k, cache_v, mask):
+    def core(self, qk, v, pos, cos, sin, cache_k, cache_v, scores):
         """Attention of the new positions over the cache: [1, T, heads d], before o_proj.
 
         pos int64 [T] positions; cos / sin [T, 1, d] RoPE rows of those positions (sin with the
         rotate-half sign folded in); cache_k / cache_v [kv_heads, max_seq, d] slabs, the key slab
-        holding K transposed ([kv_heads, d, max_seq]); mask [rep * T, max_seq], the additive causal
-        mask repeated for the rep = heads / kv_heads query heads of a KV head."""
-        return self.attend(self.rope_cache(qk, v, pos, cos, sin, cache_k, cache_v), cache_k, cache_v, mask)
+        holding K transposed ([kv_heads, d, max_seq]); scores [kv_heads, rep * T, max_seq] holding
+        the additive causal mask repeated for the rep = heads / kv_heads query heads of a KV head,
+        overwritten with the scores (see attend)."""
+        return self.attend(self.rope_cache(qk, v, pos, cos, sin, cache_k, cache_v), cache_k, cache_v, scores)
 
     def rope_cache(self, qk, v, pos, cos, sin, cache_k, cache_v):
         """RoPE on q and k, k and v written into the caches at `pos`; returns q [T, heads, d]."""
@@ -162,8 +163,12 @@ class Attention(nn.Module):
         cache_v.index_copy_(1, pos, v.view(t, hkv, d).transpose(0, 1))
         return q
 
-    def attend(self, q, cache_k, cache_v, mask):
-        """q [T, heads, d] (rotated) over the caches: [1, T, heads d], before o_proj."""
+    def attend(self, q, cache_k, cache_v, scores):
+        """q [T, heads, d] (rotated) over the caches: [1, T, heads d], before o_proj.
+
+        scores: [kv_heads, rep * T, max_seq] holding the mask on entry; the scaled products are
+        added to it in place (baddbmm_ with C = D), which spares the copy of the mask into a fresh
+        output that an out-of-place baddbmm makes in every layer (same values)."""
         cfg = self.cfg
         t = q.shape[0]
         hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
@@ -171,15 +176,15 @@ class Attention(nn.Module):
         # Query head h reads KV head h // rep: the rep heads of a KV head (and their T positions)
         # form the rows of one batch entry, so K and V are never repeated.
         qg = q.reshape(t, hkv, rep, d).permute(1, 2, 0, 3).reshape(hkv, rep * t, d)
-        scores = torch.baddbmm(mask, qg, cache_k.view(hkv, d, cfg.max_seq), alpha=1.0 / math.sqrt(d))
+        scores = scores.baddbmm_(qg, cache_k.view(hkv, d, cfg.max_seq), alpha=1.0 / math.sqrt(d))
         probs = torch.softmax(scores, dim=-1)                            # fp32 inside
         out = torch.bmm(probs, cache_v)                                  # [hkv, rep * T, d]
         return out.view(hkv, rep, t, d).permute(2, 0, 1, 3).reshape(1, t, hq * d)
 
-    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask):
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, scores):
         """x [1, T, H] (already normalized); see core for the other arguments."""
         qk, v = self.project(x)
-        return self.o_proj(self.core(qk, v, pos, cos, sin, cache_k, cache_v, mask))
+        return self.o_proj(self.core(qk, v, pos, cos, sin, cache_k, cache_v, scores))
 
 
 class MLP(nn.Module):
@@ -224,8 +229,9 @@ class DecoderLayer(nn.Module):
         return all(isinstance(p, (KFLinearInt4, FusedInt4Linear)) and getattr(p, "bias", None) is None
                    for p in qkv + gu + [a.o_proj, m.down_proj])
 
-    def forward(self, x, pos, cos, sin, cache_k, cache_v, mask, rope16=None):
-        """rope16: the full fp16 (cos, sin) tables, for the fused q|k|v launch of a decode step."""
+    def forward(self, x, pos, cos, sin, cache_k, cache_v, scores, rope16=None):
+        """scores: this layer's mask-filled score buffer (Attention.attend); rope16: the full fp16
+        (cos, sin) tables, for the fused q|k|v launch of a decode step."""
         a, m = self.self_attn, self.mlp
         if self.int4_fusable():
             # Four INT4 launches per layer at decode: RMSNorm inside q|k|v and gate|up, the residual
@@ -238,14 +244,14 @@ class DecoderLayer(nn.Module):
                                             sin=rope16[1], pos=pos, cache_k=cache_k, cache_v=cache_v, heads=c.heads,
                                             kv_heads=c.kv_heads, head_dim=c.head_dim, norm_weight=ln1.weight,
                                             eps=ln1.eps)
-                out = a.attend(y[..., :c.heads * c.head_dim].view(1, c.heads, c.head_dim), cache_k, cache_v, mask)
+                out = a.attend(y[..., :c.heads * c.head_dim].view(1, c.heads, c.head_dim), cache_k, cache_v, scores)
             else:
                 qk, v = a.project(x, ln1)
-                out = a.core(qk, v, pos, cos, sin, cache_k, cache_v, mask)
+                out = a.core(qk, v, pos, cos, sin, cache_k, cache_v, scores)
             x = _int4_fused(a.o_proj, out, residual=x)
             g, u = m.project(x, self.post_attention_layernorm)
             return _int4_fused(m.down_proj, g, up=u, residual=x)
-        x = x + a(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, mask)
+        x = x + a(self.input_layernorm(x), pos, cos, sin, cache_k, cache_v, scores)
         return x + m(self.post_attention_layernorm(x))
 
 
@@ -279,13 +285,18 @@ class TinyLlama(nn.Module):
 
     @torch.no_grad()
     def forward(self, tokens, pos, cache, rope, mask):
-        """tokens int64 [T]; pos int64 [T]; returns logits of the last position, [vocab] fp32.
-        Inference only (no autograd)."""
+        """tokens int64 [T]; pos int64 [T]; mask [T, max_seq] additive (0 / -inf); returns logits of
+        the last position, [vocab] fp32.  Inference only (no autograd)."""
         cos, sin = rope
         x = self.embed_tokens(tokens).unsqueeze(0)
-        # Per-token inputs shared by every layer: RoPE rows of the positions, and the mask
-        # repeated for the query heads that share a KV head.
-        mask_g = mask.to(x.dtype).repeat(self.cfg.heads // self.cfg.kv_heads, 1)
+        # Per-token inputs shared by every layer: RoPE rows of the positions, and every layer's
+        # score buffer filled with the mask (repeated for the query heads that share a KV head) by
+        # one copy; each layer adds its scores to its own buffer in place.
+        c_ = self.cfg
+        t, rep = tokens.numel(), c_.heads // c_.kv_heads
+        scores = mask.to(x.dtype).view(1, 1, 1, t, c_.max_seq).expand(c_.layers, c_.kv_heads, rep, t, c_.max_seq)
+        # contiguous() materializes the broadcast (reshape alone would stay a stride-0 view at T = 1).
+        scores = scores.contiguous().view(c_.layers, c_.kv_heads, rep * t, c_.max_seq)
         rope16 = (cos.to(x.dtype), sin.to(x.dtype)) if x.is_cuda and tokens.numel() == 1 else None
         # The per-position rows are only needed by layers that apply RoPE in torch.
         if rope16 is not None and all(ly.int4_fusable() and ly.self_attn.qkv is not None for ly in self.layers):
@@ -293,7 +304,7 @@ class TinyLlama(nn.Module):
         else:
             c, s = cos[pos].to(x.dtype).unsqueeze(1), sin[pos].to(x.dtype).unsqueeze(1)
         for i, layer in enumerate(self.layers):
-            x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], mask_g, rope16)
+            x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], scores[i], rope16)
         x = self.norm(x[:, -1:])
         return self.lm_head(x).float().view(-1)
 
@@ -338,6 +349,10 @@ class GraphDecoder:
         self.token = torch.zeros(1, dtype=torch.long, device=device)
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
         self.history = torch.zeros(cfg.max_seq, dtype=torch.long, device=device)
+        # The decode step's additive mask [1, max_seq] in the activation dtype: 0 for the cache
+        # slots written so far, -inf past them.  Each step opens its own slot (one index_fill_ on
+        # the device position) instead of building the mask anew.
+        self.mask = torch.full((1, cfg.max_seq), float("-inf"), dtype=model.embed_tokens.weight.dtype, device=device)
         self.graph = None
         self.host_pos = 0
 
@@ -349,12 +364,12 @@ class GraphDecoder:
                              f"{self.host_pos + steps}, past max_seq - 1 = {last}")
 
     def _step(self):
-        mask = causal_mask(self.pos, self.model.cfg.max_seq)
-        logits = self.model(self.token, self.pos, self.cache, self.rope, mask)
+        self.mask.index_fill_(1, self.pos, 0.0)
+        logits = self.model(self.token, self.pos, self.cache, self.rope, self.mask)
         nxt = torch.argmax(logits).view(1)
-        self.history.index_copy_(0, self.pos + 1, nxt)
-        self.token.copy_(nxt)
         self.pos.add_(1)
+        self.history.index_copy_(0, self.pos, nxt)
+        self.token.copy_(nxt)
 
     def prefill(self, prompt: torch.Tensor) -> None:
         """Runs the prompt eagerly; leaves the first generated token in self.token."""
@@ -369,11 +384,13 @@ class GraphDecoder:
         self.token.copy_(torch.argmax(logits).view(1))
         self.history[t] = self.token[0]
         self.pos.fill_(t)
+        self.mask.fill_(float("-inf"))
+        self.mask[:, :t] = 0.0
         self.host_pos = t
 
     def capture(self) -> None:
         self._reserve(2, "capture (two warm-up steps)")
-        saved = (self.cache.clone(), self.token.clone(), self.pos.clone(), self.history.clone())
+        saved = (self.cache.clone(), self.token.clone(), self.pos.clone(), self.history.clone(), self.mask.clone())
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -388,6 +405,7 @@ class GraphDecoder:
         self.token.copy_(saved[1])
         self.pos.copy_(saved[2])
         self.history.copy_(saved[3])
+        self.mask.copy_(saved[4])
 
     def decode(self, steps: int, use_graph: bool = True) -> torch.Tensor:
         self._reserve(steps, "decode")
