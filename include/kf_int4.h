@@ -241,6 +241,18 @@ int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream);
  * csrc/micro/bandwidth.cu:17-42's). */
 int kf_bw_read_store(const void* src, void* out, size_t bytes, int grid_blocks, void* stream);
 
+/* The greedy step of a graph-captured decode loop, one launch: idx = argmax(logits[0..n)) over
+ * fp16 logits in torch.argmax's order (NaN above every number; among equal values the smallest
+ * index), then p = *pos + 1; *pos = p; *token = idx; and, when 0 <= p < max_seq,
+ * history[p] = idx and (mask non-NULL) mask[p] = 0 (fp16), so the next step's additive mask
+ * admits its own position.  token, pos, history: int64 on the device; every write stays inside
+ * history[0, max_seq) and mask[0, max_seq).  Replaces torch's argmax, fp32 cast and the
+ * index / copy / add kernels of the decoder's step (kernelforge/tinyllama.py, config 5 of the
+ * benchmark); no reference counterpart (the reference's harness does these in torch,
+ * bench/e2e_model.py:85-141). */
+int kf_decode_argmax_step(const void* logits, int n, void* token, void* pos, void* history, int max_seq,
+                          void* mask, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -426,6 +426,21 @@ int kf_bw_read_store(const void* src, void* out, size_t bytes, int grid_blocks, 
                     "bw_read_store");
 }
 
+int kf_decode_argmax_step(const void* logits, int n, void* token, void* pos, void* history, int max_seq, void* mask,
+                          void* stream) {
+  if (!logits || !token || !pos || !history)
+    return fail(KF_ERR_INVALID_ARG, "logits, token, pos and history must be non-null");
+  if (n < 1 || max_seq < 1) return fail(KF_ERR_INVALID_ARG, "n and max_seq must be positive, got n=%d max_seq=%d", n,
+                                        max_seq);
+  if (!aligned(logits, 2) || (mask && !aligned(mask, 2)))
+    return fail(KF_ERR_INVALID_ARG, "logits and mask must be 2-byte aligned");
+  if (!aligned(token, 8) || !aligned(pos, 8) || !aligned(history, 8))
+    return fail(KF_ERR_INVALID_ARG, "token, pos and history must be 8-byte aligned");
+  return hip_status(kf::decode_argmax_launch(logits, n, token, pos, history, max_seq, mask,
+                                             static_cast<hipStream_t>(stream)),
+                    "decode_argmax_step launch");
+}
+
 int kf_bw_write(void* dst, size_t bytes, int grid_blocks, void* stream) {
   int st = bw_args(dst, bytes, &grid_blocks);
   if (st) return st;

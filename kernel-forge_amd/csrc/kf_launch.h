@@ -190,6 +190,8 @@ hipError_t bw_copy_launch(const void* src, void* dst, size_t bytes, int grid, hi
 hipError_t bw_read_launch(const void* src, void* sink, size_t bytes, int grid, hipStream_t stream);
 hipError_t bw_read_store_launch(const void* src, void* out, size_t bytes, int grid, hipStream_t stream);
 hipError_t bw_write_launch(void* dst, size_t bytes, int grid, hipStream_t stream);
+hipError_t decode_argmax_launch(const void* logits, int n, void* token, void* pos, void* history, int max_seq,
+                                void* mask, hipStream_t stream);
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -70,6 +70,7 @@ SIGNATURES = {
     "kf_bw_read": (_I, [_VP, _VP, _SZ, _I, _VP]),
     "kf_bw_write": (_I, [_VP, _SZ, _I, _VP]),
     "kf_bw_read_store": (_I, [_VP, _VP, _SZ, _I, _VP]),
+    "kf_decode_argmax_step": (_I, [_VP, _I, _VP, _VP, _VP, _I, _VP, _VP]),
 }
 
 _lib: ctypes.CDLL | None = None

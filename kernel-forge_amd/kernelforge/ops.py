@@ -656,3 +656,35 @@ def _int4_qkv_rope_cache_op(x: torch.Tensor, packed: torch.Tensor, scales: torch
 def _(x, packed, scales, group_size, cos, sin, pos, cache_k, cache_v, heads, kv_heads, head_dim, norm_weight, eps):
     return x.new_empty(1, packed.shape[0])
 
+
+
+def decode_argmax_step(logits: torch.Tensor, token: torch.Tensor, pos: torch.Tensor, history: torch.Tensor,
+                       mask: torch.Tensor | None = None) -> None:
+    """The greedy step of a graph-captured decode loop in one launch (kf_decode_argmax_step).
+
+    logits: fp16 [n] on the GPU; token, pos: int64 [1]; history: int64 [max_seq]; mask: None or
+    fp16 with max_seq elements.  Computes idx = torch.argmax(logits) (same tie and NaN rules) and
+    then, on the device: pos += 1; token = idx; history[pos] = idx and mask[pos] = 0 when pos <
+    max_seq.  Asynchronous on the current stream; capturable.  No reference counterpart (the
+    reference's decode loop does these steps as separate torch ops).
+    """
+    if logits.dtype != torch.float16 or logits.dim() != 1 or not logits.is_cuda or not logits.is_contiguous():
+        raise TypeError("logits must be a contiguous 1-D fp16 CUDA tensor")
+    for name, t in (("token", token), ("pos", pos)):
+        if t.dtype != torch.int64 or t.numel() != 1 or t.device != logits.device:
+            raise ValueError(f"{name} must be one int64 on {logits.device}")
+    if history.dtype != torch.int64 or history.dim() != 1 or not history.is_contiguous() or \
+            history.device != logits.device:
+        raise ValueError(f"history must be a contiguous 1-D int64 tensor on {logits.device}")
+    max_seq = history.numel()
+    if mask is not None and (mask.dtype != torch.float16 or mask.numel() != max_seq or not mask.is_contiguous()
+                             or mask.device != logits.device):
+        raise ValueError(f"mask must be a contiguous fp16 tensor of {max_seq} elements on {logits.device}")
+    if _traced((logits, token, pos, history, mask)):
+        raise RuntimeError("decode_argmax_step updates device buffers in place and has no traceable form")
+    lib = _lib.load()
+    with _on(logits.device):
+        status = lib.kf_decode_argmax_step(_ptr(logits), logits.numel(), _ptr(token), _ptr(pos), _ptr(history),
+                                           max_seq, _ptr(mask) if mask is not None else None,
+                                           _stream_ptr(logits.device))
+    _lib.check(status, "decode_argmax_step")

@@ -284,9 +284,10 @@ class TinyLlama(nn.Module):
         return torch.zeros(c.layers, 2, c.kv_heads, c.max_seq, c.head_dim, device=device, dtype=dtype)
 
     @torch.no_grad()
-    def forward(self, tokens, pos, cache, rope, mask):
+    def forward(self, tokens, pos, cache, rope, mask, logits_fp32: bool = True):
         """tokens int64 [T]; pos int64 [T]; mask [T, max_seq] additive (0 / -inf); returns logits of
-        the last position, [vocab] fp32.  Inference only (no autograd)."""
+        the last position, [vocab], fp32 (or the lm_head's own dtype with logits_fp32=False).
+        Inference only (no autograd)."""
         cos, sin = rope
         x = self.embed_tokens(tokens).unsqueeze(0)
         # Per-token inputs shared by every layer: RoPE rows of the positions, and every layer's
@@ -306,7 +307,8 @@ class TinyLlama(nn.Module):
         for i, layer in enumerate(self.layers):
             x = layer(x, pos, c, s, cache[i, 0], cache[i, 1], scores[i], rope16)
         x = self.norm(x[:, -1:])
-        return self.lm_head(x).float().view(-1)
+        logits = self.lm_head(x).view(-1)
+        return logits.float() if logits_fp32 else logits
 
 
 def causal_mask(pos: torch.Tensor, max_seq: int) -> torch.Tensor:
@@ -350,8 +352,9 @@ class GraphDecoder:
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
         self.history = torch.zeros(cfg.max_seq, dtype=torch.long, device=device)
         # The decode step's additive mask [1, max_seq] in the activation dtype: 0 for the cache
-        # slots written so far, -inf past them.  Each step opens its own slot (one index_fill_ on
-        # the device position) instead of building the mask anew.
+        # slots up to the current position, -inf past them.  Prefill opens the prompt's slots and
+        # the first decode position's; every step opens the next one, so the mask is never built
+        # anew.
         self.mask = torch.full((1, cfg.max_seq), float("-inf"), dtype=model.embed_tokens.weight.dtype, device=device)
         self.graph = None
         self.host_pos = 0
@@ -364,12 +367,17 @@ class GraphDecoder:
                              f"{self.host_pos + steps}, past max_seq - 1 = {last}")
 
     def _step(self):
-        self.mask.index_fill_(1, self.pos, 0.0)
+        if self.token.is_cuda:
+            # argmax over the fp16 logits, pos += 1, history / token / mask updates: one launch.
+            logits = self.model(self.token, self.pos, self.cache, self.rope, self.mask, logits_fp32=False)
+            ops.decode_argmax_step(logits, self.token, self.pos, self.history, self.mask)
+            return
         logits = self.model(self.token, self.pos, self.cache, self.rope, self.mask)
         nxt = torch.argmax(logits).view(1)
         self.pos.add_(1)
         self.history.index_copy_(0, self.pos, nxt)
         self.token.copy_(nxt)
+        self.mask.index_fill_(1, self.pos, 0.0)
 
     def prefill(self, prompt: torch.Tensor) -> None:
         """Runs the prompt eagerly; leaves the first generated token in self.token."""
@@ -385,7 +393,7 @@ class GraphDecoder:
         self.history[t] = self.token[0]
         self.pos.fill_(t)
         self.mask.fill_(float("-inf"))
-        self.mask[:, :t] = 0.0
+        self.mask[:, :t + 1] = 0.0
         self.host_pos = t
 
     def capture(self) -> None:

@@ -97,6 +97,18 @@ def test_gemm_argument_errors_without_gpu():
     assert lib.kf_int4_gemm_workspace_bytes(0, 64, 256, 128) == 0
 
 
+def test_decode_argmax_step_argument_errors_without_gpu():
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    _err(lib.kf_decode_argmax_step(None, 16, p, p, p, 8, None, None), "non-null")
+    _err(lib.kf_decode_argmax_step(p, 16, p, None, p, 8, None, None), "non-null")
+    _err(lib.kf_decode_argmax_step(p, 0, p, p, p, 8, None, None), "positive")
+    _err(lib.kf_decode_argmax_step(p, 16, p, p, p, 0, None, None), "positive")
+    _err(lib.kf_decode_argmax_step(ctypes.c_void_p(0x1001), 16, p, p, p, 8, None, None), "2-byte aligned")
+    _err(lib.kf_decode_argmax_step(p, 16, p, p, p, 8, ctypes.c_void_p(0x1003), None), "2-byte aligned")
+    _err(lib.kf_decode_argmax_step(p, 16, ctypes.c_void_p(0x1004), p, p, 8, None, None), "8-byte aligned")
+
+
 def test_fused_gemv_argument_errors_without_gpu():
     lib = _lib.load()
     p = ctypes.c_void_p(0x1000)
