@@ -303,11 +303,8 @@ EDGE_CASES = [(513, 2112, 384), (1000, 320, 4224), (1000, 2112, 384), (1500, 640
               (130, 1600, 640), (65, 192, 4160), (900, 1472, 6272), (600, 1216, 7424), (1300, 6080, 640)]
 
 
-@pytest.mark.parametrize("m,n,k", EDGE_CASES)
-@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("m,n,k,group", [(m, n, k, g) for m, n, k in EDGE_CASES for g in (64, 128) if k % g == 0])
 def test_gemm_edge_shapes_every_tile(error_log, m, n, k, group):
-    if k % group:
-        pytest.skip("K not a multiple of the group")
     _check(error_log, "int4_gemm", ops.int4_gemm, m, n, k, group, f"edge_{m}x{n}x{k}")
 
 
