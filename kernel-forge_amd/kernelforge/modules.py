@@ -85,20 +85,29 @@ class _SiblingLaunch:
     The first sibling called on an input launches the group (one GEMV launch at decode sizes, the
     per-problem kernels above them: every output is bit-identical to the sibling's own
     int4_linear) and keeps the other outputs until their modules are called with that same input
-    object.  A call with another input while outputs are still waiting means the caller does not
-    call the siblings on one input: the waiting outputs are dropped and that call runs on its own,
-    so results never depend on the call pattern, only the launch count does.  Holds references to
-    the input and outputs only until the last sibling has taken its output."""
+    object.  A call with another input while outputs are still waiting - another tensor, or the
+    same tensor updated in place since (its version counter moved; tensors made under
+    torch.inference_mode() keep no counter, so for them only identity is checked) - means the
+    caller does not call the siblings on one input: the waiting outputs are dropped and that call
+    runs on its own, so results never depend on the call pattern, only the launch count does.
+    Holds references to the input and outputs only until the last sibling has taken its output."""
 
     def __init__(self, members: list[KFLinearInt4]):
         self.members = members
         self._x: torch.Tensor | None = None
+        self._version: int | None = None
         self._ys: list[torch.Tensor] | None = None
         self._pending: set[int] = set()
 
+    @staticmethod
+    def _version_of(x: torch.Tensor) -> int | None:
+        """x's version counter (bumped by every in-place update), None for inference tensors,
+        which keep none."""
+        return None if x.is_inference() else x._version
+
     def output(self, slot: int, x: torch.Tensor) -> torch.Tensor:
         if self._pending:
-            if x is self._x and slot in self._pending:
+            if x is self._x and slot in self._pending and self._version_of(x) == self._version:
                 y = self._ys[slot]
                 self._pending.discard(slot)
                 if not self._pending:
@@ -111,6 +120,7 @@ class _SiblingLaunch:
         ys = ops.int4_linear_grouped([x] * len(ms), [m.packed for m in ms], [m.scales for m in ms],
                                      ms[0].group_size, [m.bias for m in ms])
         self._x, self._ys, self._pending = x, ys, set(range(len(ms))) - {slot}
+        self._version = self._version_of(x)
         return ys[slot]
 
 

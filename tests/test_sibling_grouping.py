@@ -127,3 +127,19 @@ def test_mismatched_siblings_are_not_grouped():
     blk.self_attn.v_proj = modules.KFLinearInt4(kq.quantize_weight(torch.ones(32, 2 * K) * 0.01, G), None)
     blk.mlp.up_proj = modules.KFLinearInt4(kq.quantize_weight(torch.ones(96, K) * 0.01, 64), None)
     assert modules.group_sibling_linears_(blk) == 0
+
+
+def test_input_updated_in_place_between_siblings_is_not_paired(launches):
+    blk = _Block()
+    modules.group_sibling_linears_(blk)
+    g, u = blk.mlp.gate_proj, blk.mlp.up_proj
+    x = _x(1.0)
+    g(x)
+    x.fill_(3.0)                          # same object, new contents: the waiting output is stale
+    assert u(x)[0, 0, 0] == 96 * 1000 + 3
+    assert launches == [("grouped", (96, 96)), ("single", 96)]
+    with torch.inference_mode():          # no version counter: identity alone pairs the calls
+        xi = _x(5.0)
+        g(xi)
+        assert u(xi)[0, 0, 0] == 96 * 1000 + 5
+    assert launches[-1] == ("grouped", (96, 96))
