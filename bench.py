@@ -114,6 +114,10 @@ def parse_args():
     ap.add_argument("--no-quant", action="store_true", help="skip the on-device quantize leg")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the ceilings and the timed grouped step (the command profiles/ traces)")
+    ap.add_argument("--power", action="store_true",
+                    help="only the board power / clock of the M=2048 gate GEMM run back to back (INT4 and "
+                         "hipBLASLt fp16), from amd-smi samples; prints one JSON line")
+    ap.add_argument("--power-seconds", type=float, default=3.0)
     return ap.parse_args()
 
 
@@ -708,6 +712,100 @@ def environment(torch, props) -> dict:
     return env
 
 
+def _board_sample() -> tuple[float, float] | None:
+    """(socket power W, mean gfx clock MHz over the XCDs) from one `amd-smi metric` read."""
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c", "--json"], capture_output=True,
+                             text=True, timeout=5)
+        d = json.loads(out.stdout)
+        g = d[0] if isinstance(d, list) else d["gpu_data"][0]
+        clocks = [c["clk"]["value"] for k, c in g["clock"].items()
+                  if k.startswith("gfx_") and isinstance(c, dict) and isinstance(c.get("clk"), dict)]
+        return float(g["power"]["socket_power"]["value"]), float(statistics.mean(clocks))
+    except (OSError, subprocess.SubprocessError, ValueError, KeyError, TypeError, statistics.StatisticsError):
+        return None
+
+
+def power_leg(torch, ops, kq, seconds: float) -> dict:
+    """Board power and shader clock while the M=2048 gate GEMM runs back to back.
+
+    The INT4 GEMM (weights of the bench's gate layer, resident) and hipBLASLt's fp16 GEMM on the
+    same shape each replay a graph of 20 launches for `seconds`; a thread reads `amd-smi metric`
+    every 50 ms, and the medians of the samples after the first 0.5 s of each run are reported
+    with the per-launch time (HIP events around all replays) and the rate.  Two rounds, then the
+    idle board.  The GEMM's speed is set by the clock the board's power limit allows, which this
+    shows."""
+    import threading
+
+    samples: list = []
+    stop = threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            v = _board_sample()
+            if v is not None:
+                samples.append((time.time(), *v))
+            time.sleep(0.05)
+
+    layers = make_layers(torch, kq)
+    gate = [ly for ly in layers if ly["name"] == "gate"][0]
+    p, s_ = gate["packed"].cuda(), gate["scales"].cuda()
+    m, n, k = 2048, gate["N"], gate["K"]
+    x = torch.randn(m, k, dtype=torch.float16, device="cuda")
+    wf = (torch.randn(n, k, device="cuda") * 0.02).half()
+
+    def graph_of(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(20):
+                fn()
+        return g
+
+    graphs = {"int4_gemm": graph_of(lambda: ops.int4_gemm(x, p, s_, GROUP)),
+              "hipblaslt_fp16": graph_of(lambda: torch.nn.functional.linear(x, wf))}
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    out: dict = {"shape": [m, n, k], "launches_per_replay": 20, "seconds": seconds, "runs": []}
+    try:
+        time.sleep(1.5)
+        for rnd in range(2):
+            for name, g in graphs.items():
+                torch.cuda.synchronize()
+                t0 = time.time()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                reps = 0
+                while time.time() - t0 < seconds:
+                    g.replay()
+                    reps += 1
+                    if reps % 20 == 0:
+                        torch.cuda.synchronize()
+                b.record()
+                torch.cuda.synchronize()
+                t1 = time.time()
+                us = a.elapsed_time(b) * 1e3 / (reps * 20)
+                sel = [q for q in samples if t0 + 0.5 <= q[0] <= t1]
+                out["runs"].append({
+                    "kernel": name, "round": rnd, "us_per_launch": round(us, 2),
+                    "tflops": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
+                    "power_w": statistics.median([q[1] for q in sel]) if sel else None,
+                    "gfx_mhz": round(statistics.median([q[2] for q in sel])) if sel else None, "samples": len(sel)})
+                log(f"power: {out['runs'][-1]}")
+                time.sleep(1.5)
+        idle = [q for q in samples if q[0] >= time.time() - 1.0]
+        out["idle_power_w"] = statistics.median([q[1] for q in idle]) if idle else None
+    finally:
+        stop.set()
+        th.join(timeout=10)
+    return out
+
+
 def host_enqueue_us(torch, fn, calls: int = 200) -> float:
     """Host time per eager call (launch enqueue, no synchronization), median of 5 batches."""
     for _ in range(20):
@@ -774,7 +872,7 @@ def main() -> int:
         return 2
     full = not args.headline_only
     traffic = None
-    if full and not args.profile and not args.no_traffic:
+    if full and not args.profile and not args.power and not args.no_traffic:
         log("rocprofv3 FETCH_SIZE / WRITE_SIZE passes (child processes)")
         traffic = measure_traffic()
         log(f"traffic: {traffic}")
@@ -793,6 +891,9 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     if args.profile:
         return profile_only(args, torch, lib, kl, ops, kq)
+    if args.power:
+        print(json.dumps({"power_m2048": power_leg(torch, ops, kq, args.power_seconds)}), flush=True)
+        return 0
 
     log("measuring HBM ceilings")
     ceil = measure_hbm(torch, lib, kl)
