@@ -66,11 +66,12 @@ int cu_count(int* out) {
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 // Checks shared by the GEMV and the GEMM (order and wording follow
-// kernelforge/ops.py:171-182 and csrc/gemm/dequant_gemv.cu:5-19).
+// kernelforge/ops.py:171-182 and csrc/gemm/dequant_gemv.cu:5-19).  The sizes come before the
+// pointers: an empty tensor's data pointer is null, and its size is the error worth naming.
 int check_common(const void* x, const void* packed, const void* scales, const void* y, int M, int N, int K,
                  int group_size) {
-  if (!x || !packed || !scales || !y) return fail(KF_ERR_INVALID_ARG, "x, packed, scales and y must be non-null");
   if (M < 1 || N < 1 || K < 1) return fail(KF_ERR_INVALID_ARG, "M, N, K must be positive, got M=%d N=%d K=%d", M, N, K);
+  if (!x || !packed || !scales || !y) return fail(KF_ERR_INVALID_ARG, "x, packed, scales and y must be non-null");
   if (N > KF_MAX_ROWS) return fail(KF_ERR_UNSUPPORTED, "N=%d exceeds the %d rows one launch supports", N, KF_MAX_ROWS);
   if (group_size != 64 && group_size != 128)
     return fail(KF_ERR_INVALID_ARG, "group_size must be one of (64, 128), got %d", group_size);

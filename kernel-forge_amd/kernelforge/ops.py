@@ -242,6 +242,8 @@ def int4_gemm(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, group
     if packed.shape[0] % 64 != 0:
         raise ValueError(f"int4_gemm needs N to be a multiple of 64, got N={packed.shape[0]}")
     _check_native(x, packed, scales, group_size)
+    if x.shape[0] < 1:  # csrc/gemm/dequant_gemm_tc.cu:14 (its TORCH_CHECK text)
+        raise RuntimeError(f"bad M {x.shape[0]}")
     return _launch_gemm(x, packed, scales, int(group_size))
 
 

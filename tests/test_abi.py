@@ -50,6 +50,9 @@ def test_gemv_argument_errors_without_gpu():
     _err(lib.kf_int4_gemv(p, p, p, p, 1, 64, 256, 32, None), "group_size")
     _err(lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None), r"M in \[1, 8\]")
     _err(lib.kf_int4_gemv(p, p, p, p, 0, 64, 256, 128, None), "positive")
+    # empty tensors have null data pointers: their sizes are what the error names
+    _err(lib.kf_int4_gemv(p, None, None, None, 1, 0, 256, 128, None), "positive, got M=1 N=0")
+    _err(lib.kf_int4_gemm(None, p, p, None, None, 0, 0, 128, 256, 128, None), "positive, got M=0")
     _err(lib.kf_int4_gemv(ctypes.c_void_p(0x1002), p, p, p, 1, 64, 256, 128, None), "16-byte aligned")
     with pytest.raises(ValueError, match=r"M in \[1, 8\]"):
         _lib.check(lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None), "int4_gemv")

@@ -111,6 +111,29 @@ def test_gemv_rejects_shape_mismatch():
         ops.int4_gemv(x[:, :128].contiguous(), dp, ds, 128)
 
 
+def test_degenerate_shapes():
+    """M = 0 raises what the reference raises: int4_gemv's M check, reached from int4_linear
+    (2-D and 3-D x) and int4_matmul, and int4_gemm's "bad M" (csrc/gemm/dequant_gemm_tc.cu:14).
+    N = 0 and K = 0, for which the reference's GEMV fails its launch or sums nothing and its
+    GEMM's split choice divides by zero, raise the C ABI's size error here."""
+    _, _, dp, ds = _weights(64, 256, 128)
+    x0 = torch.empty(0, 256, device=DEV, dtype=torch.float16)
+    for fn in (ops.int4_gemv, ops.int4_matmul, ops.int4_linear):
+        with pytest.raises(ValueError, match=r"M in \[1, 8\], got M=0"):
+            fn(x0, dp, ds, 128)
+    with pytest.raises(ValueError, match="got M=0"):
+        ops.int4_linear(torch.empty(2, 0, 256, device=DEV, dtype=torch.float16), dp, ds, 128)
+    with pytest.raises(RuntimeError, match="bad M 0"):
+        ops.int4_gemm(x0, dp, ds, 128)
+    x = torch.randn(1, 256, device=DEV).half()
+    with pytest.raises(ValueError, match="positive, got M=1 N=0 K=256"):
+        ops.int4_gemv(x, dp[:0], ds[:0], 128)
+    with pytest.raises(ValueError, match="positive, got M=1 N=64 K=0"):
+        ops.int4_gemv(x[:, :0], dp[:, :0], ds[:, :0], 128)
+    with pytest.raises(ValueError, match="positive, got M=16 N=64 K=0"):
+        ops.int4_gemm(torch.empty(16, 0, device=DEV, dtype=torch.float16), dp[:, :0], ds[:, :0], 128)
+
+
 def test_rejects_cpu_and_wrong_dtype():
     _, _, dp, ds = _weights(64, 256, 128)
     with pytest.raises(TypeError, match="fp16 CUDA"):
