@@ -251,3 +251,33 @@ def test_gemv_plan_argument_errors_without_gpu():
     _err(lib.kf_int4_gemv_plan(9, one, k, 1, CUS, None, None, None, None), r"M in \[1, 8\]")
     bad = (ctypes.c_int * 1)(200)
     _err(lib.kf_int4_gemv_plan(1, one, bad, 1, CUS, None, None, None, None), "multiple of 64")
+
+
+def test_last_error_is_per_thread():
+    """kf_last_error names the calling thread's own most recent failure: two threads that fail
+    differently, interleaved, each read back their own message."""
+    import threading
+
+    lib = _lib.load()
+    p = ctypes.c_void_p(0x1000)
+    barrier = threading.Barrier(2)
+    seen = {}
+
+    def worker(name, call, want):
+        barrier.wait()
+        assert call() != 0
+        barrier.wait()  # both threads have failed before either reads its message
+        seen[name] = (_lib.last_error(), want)
+
+    threads = [threading.Thread(target=worker, args=("group", lambda: lib.kf_int4_gemv(p, p, p, p, 1, 64, 256, 32, None),
+                                                     "group_size")),
+               threading.Thread(target=worker, args=("m", lambda: lib.kf_int4_gemv(p, p, p, p, 9, 64, 256, 128, None),
+                                                     r"M in \[1, 8\]"))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert set(seen) == {"group", "m"}
+    for msg, want in seen.values():
+        assert re.search(want, msg), msg
+    assert not re.search(r"M in \[1, 8\]", seen["group"][0]) and "group_size" not in seen["m"][0]
