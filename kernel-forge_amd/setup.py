@@ -16,18 +16,33 @@ from pathlib import Path
 
 from setuptools import find_packages, setup
 from setuptools.command.build_py import build_py
+from setuptools.command.develop import develop
 
 HERE = Path(__file__).resolve().parent
 
 
+def _build_library() -> None:
+    spec = importlib.util.spec_from_file_location("kf_build", HERE / "kernelforge" / "build.py")
+    builder = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(builder)
+    print(f"built {builder.build_library()}")
+
+
 class BuildWithLibrary(build_py):
-    """build_py that first builds libkf_int4.so in the source tree."""
+    """build_py (wheels, and editable installs on setuptools >= 64) that first builds
+    libkf_int4.so in the source tree."""
 
     def run(self):
-        spec = importlib.util.spec_from_file_location("kf_build", HERE / "kernelforge" / "build.py")
-        builder = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(builder)
-        print(f"built {builder.build_library()}")
+        _build_library()
+        super().run()
+
+
+class DevelopWithLibrary(develop):
+    """The legacy editable install (``setup.py develop``, which pip falls back to on older
+    setuptools) runs no build_py: build the library here as well."""
+
+    def run(self):
+        _build_library()
         super().run()
 
 
@@ -39,5 +54,5 @@ setup(
     package_data={"kernelforge": ["libkf_int4.so"]},
     python_requires=">=3.10",
     install_requires=["torch", "numpy"],
-    cmdclass={"build_py": BuildWithLibrary},
+    cmdclass={"build_py": BuildWithLibrary, "develop": DevelopWithLibrary},
 )

@@ -6,8 +6,8 @@ from __future__ import annotations
 import os
 from pathlib import Path
 
-from setuptools import distutils  # noqa: F401  (setuptools' own distutils, before run_setup)
-from distutils.core import run_setup
+import setuptools  # noqa: F401  (first, so that distutils below is setuptools' copy)
+from distutils.core import run_setup  # noqa: E402
 
 SETUP = Path(__file__).resolve().parents[1] / "kernel-forge_amd" / "setup.py"
 
@@ -23,3 +23,4 @@ def test_setup_declares_the_package_and_its_library():
     assert dist.packages == ["kernelforge"]
     assert dist.package_data == {"kernelforge": ["libkf_int4.so"]}
     assert dist.cmdclass["build_py"].__name__ == "BuildWithLibrary"
+    assert dist.cmdclass["develop"].__name__ == "DevelopWithLibrary"
