@@ -8,4 +8,5 @@ Submodules:
   build     hipcc build of libkf_int4.so
 """
 
+__version__ = "0.3.0"
 __all__ = ["quantize", "ops", "modules"]

@@ -12,6 +12,7 @@ the reference's package first.
 """
 
 import importlib.util
+import re
 from pathlib import Path
 
 from setuptools import find_packages, setup
@@ -19,6 +20,7 @@ from setuptools.command.build_py import build_py
 from setuptools.command.develop import develop
 
 HERE = Path(__file__).resolve().parent
+VERSION = re.search(r'^__version__ = "([^"]+)"', (HERE / "kernelforge" / "__init__.py").read_text(), re.M).group(1)
 
 
 def _build_library() -> None:
@@ -48,7 +50,7 @@ class DevelopWithLibrary(develop):
 
 setup(
     name="kernelforge-mi355x",
-    version="0.3.0",
+    version=VERSION,
     description="KernelForge's INT4 weight-only linear (ops.int4_linear) as gfx950 HIP kernels behind a C ABI",
     packages=find_packages(include=["kernelforge"]),
     package_data={"kernelforge": ["libkf_int4.so"]},

@@ -20,6 +20,8 @@ def test_setup_declares_the_package_and_its_library():
     finally:
         os.chdir(cwd)
     assert dist.get_name() == "kernelforge-mi355x"
+    import kernelforge
+    assert dist.get_version() == kernelforge.__version__
     assert dist.packages == ["kernelforge"]
     assert dist.package_data == {"kernelforge": ["libkf_int4.so"]}
     assert dist.cmdclass["build_py"].__name__ == "BuildWithLibrary"
